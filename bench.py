@@ -1,0 +1,363 @@
+"""Benchmark of the MI355X KV-cache hot path (one JSON line on stdout).
+
+Headline workload (the path's batched serving step):
+  32 sequences, lengths drawn U[128, 8192] from seed 3, 32 query / 8 KV heads,
+  head_dim 128, fp16 KV in 16-token pages whose physical ids are a seeded
+  random permutation of one shared pool.  One step = paged append of one new
+  K/V token per sequence at position L_b, then split-K decode attention of one
+  query per sequence over L_b + 1 keys.  Lengths are held fixed from step to
+  step (each step rewrites the same slot), so every timed step does identical
+  work.
+
+value = algorithmic bytes of the step (decode: K+V of every cached token once,
+q read, out write, block-table and length reads; append: new K/V read + write)
+divided by the measured step time.  roofline = the decode kernel alone, timed
+with HIP events on its stream inside the timed region.  cpu_baseline = the
+oracle's restatement of the reference CPU attention arithmetic
+(oracle/kvhp_oracle.c) on the same inputs, on the host cores.
+
+Also reported under "extra" (each measured with L2+MALL flushed by a 1 GiB
+write before every rep unless labelled warm): config 1 (decode at ctx 512),
+config 2 (ctx 4K/16K/64K x splits 1/4/16/64), config 4 (causal prefill
+S=512/2048/8192, TFLOP/s vs fp16 MFMA peak).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "serving-engine_amd"))
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+METRIC = ("decode-attn HBM GB/s (% of peak) + µs/step; 1.1B decode tok/s at ctx 2K, 1 GPU")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--splits", type=int, default=0, help="decode split count (0 = auto)")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 2 and 4")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4")
+    return ap.parse_args()
+
+
+class Flusher:
+    """Writes 1 GiB (4x the 256 MB MALL) to evict L2 and MALL between reps."""
+
+    def __init__(self, torch):
+        self.buf = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+
+    def __call__(self):
+        self.buf.zero_()
+
+
+def time_op(torch, fn, reps, flush=None):
+    """Median and mean device time (us) of fn over reps, HIP events on the
+    current stream, optional flush before each rep (outside the events)."""
+    stream = torch.cuda.current_stream()
+    times = []
+    for _ in range(reps):
+        if flush:
+            flush()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        fn()
+        e.record(stream)
+        e.synchronize()
+        times.append(s.elapsed_time(e) * 1e3)
+    return float(np.median(times)), float(np.mean(times))
+
+
+# ---------------------------------------------------------------- config 3 --
+def decode_bytes(lens, hq, hkv, d):
+    lens = np.asarray(lens, np.int64)
+    kv = int(lens.sum()) * hkv * d * 2 * 2
+    qo = 2 * len(lens) * hq * d * 2
+    table = int(((lens + 15) // 16).sum()) * 4 + len(lens) * 4
+    return kv + qo + table
+
+
+def append_bytes(b, hkv, d):
+    return b * hkv * d * 2 * 2 * 2 + b * 4 * 2
+
+
+def build_config3(torch, kvhp, seed=3):
+    b, hq, hkv, d = 32, 32, 8, 128
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(128, 8193, size=b).astype(np.int32)  # cached tokens
+    need = (lens + 1 + 15) // 16
+    P = int(need.sum()) + 16
+    maxp = int(need.max()) + 1
+    perm = rng.permutation(P).astype(np.int32)
+    bt = np.full((b, maxp), -1, np.int32)
+    o = 0
+    for i, n in enumerate(need):
+        bt[i, :n] = perm[o:o + n]
+        o += int(n)
+    dev = torch.device("cuda")
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    pool_k = torch.randn((hkv, P, 16, d), generator=g, device=dev).half()
+    pool_v = torch.randn((hkv, P, 16, d), generator=g, device=dev).half()
+    new_k = torch.randn((b, 1, hkv, d), generator=g, device=dev).half()
+    new_v = torch.randn((b, 1, hkv, d), generator=g, device=dev).half()
+    q = torch.randn((b, hq, d), generator=g, device=dev).half()
+    return dict(b=b, hq=hq, hkv=hkv, d=d, lens=lens, bt=torch.from_numpy(bt).to(dev),
+                bt_np=bt, P=P, pool_k=pool_k, pool_v=pool_v, new_k=new_k, new_v=new_v, q=q,
+                pos=torch.from_numpy(lens).to(dev),
+                lens1=torch.from_numpy(lens + 1).to(dev),
+                out=torch.empty((b, hq, d), dtype=torch.float16, device=dev))
+
+
+def cpu_baseline_config3(c, torch):
+    """Oracle decode (reference attention arithmetic restated in C) on the
+    same step's inputs, all host threads; sample = the full 32-sequence step."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    b, hq, hkv, d = c["b"], c["hq"], c["hkv"], c["d"]
+    L1 = c["lens"] + 1
+    cap = int(L1.max())
+    kv_k = torch.empty((b, hkv, cap, d), dtype=torch.float16, device="cuda")
+    kv_v = torch.empty_like(kv_k)
+    import kvhp
+    kvhp.paged_gather_kv(c["pool_k"], c["pool_v"], c["bt"], c["lens1"], cap, kv_k, kv_v)
+    torch.cuda.synchronize()
+    kf = kv_k.float().cpu().numpy()
+    vf = kv_v.float().cpu().numpy()
+    del kv_k, kv_v
+    qf = c["q"].float().cpu().numpy()
+    threads = min(16, os.cpu_count() or 1)
+    oracle.decode_attention(qf, kf[:1, :, :64], vf[:1, :, :64], np.array([64], np.int32), hq,
+                            hkv, d, threads)  # warm
+    t0 = time.perf_counter()
+    ref = oracle.decode_attention(qf, kf, vf, L1, hq, hkv, d, threads)
+    dt = time.perf_counter() - t0
+    nbytes = decode_bytes(L1, hq, hkv, d)
+    gpu_out = c["out"].float().cpu().numpy()
+    err = float(np.abs(gpu_out - ref).max())
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"full config-3 decode (32 seqs, sum L={int(L1.sum())}), 1 rep, "
+                      f"{dt:.2f} s; oracle max-abs diff vs GPU output {err:.2e}",
+            "seconds": round(dt, 3)}
+
+
+def run_config3(torch, kvhp, args):
+    c = build_config3(torch, kvhp)
+    b, hq, hkv, d = c["b"], c["hq"], c["hkv"], c["d"]
+    L1 = c["lens"] + 1
+    max_len = int(L1.max())
+    splits = args.splits or kvhp.decode_auto_splits(b, hkv, d, max_len)
+    ws_bytes = kvhp.decode_workspace_bytes(b, hq, hkv, d, max_len, splits)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device="cuda")
+    kvhp.decode_workspace_init(ws)
+    kview = kvhp.paged_view(c["pool_k"], c["bt"])
+    vview = kvhp.paged_view(c["pool_v"], c["bt"])
+    stream = torch.cuda.current_stream()
+
+    def append():
+        kvhp.paged_append_kv(c["new_k"], c["new_v"], c["pool_k"], c["pool_v"], c["bt"],
+                             c["pos"], b, 1, hkv, d)
+
+    def decode():
+        kvhp.decode_attention(c["q"], kview, vview, c["lens1"], c["out"], hq, hkv, d, max_len,
+                              splits, ws)
+
+    for _ in range(args.warmup):
+        append()
+        decode()
+    torch.cuda.synchronize()
+    n = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(n):
+        append()
+        ev[i][0].record(stream)
+        decode()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dec_us = [s.elapsed_time(e) * 1e3 for s, e in ev]
+    step_bytes = decode_bytes(L1, hq, hkv, d) + append_bytes(b, hkv, d)
+    dbytes = decode_bytes(L1, hq, hkv, d)
+    avg_dec = float(np.mean(dec_us))
+    res = {
+        "ms_per_step": wall * 1e3 / n,
+        "value": step_bytes / (wall / n) / 1e9,
+        "decode_us_mean": avg_dec,
+        "decode_us_median": float(np.median(dec_us)),
+        "decode_bytes": dbytes,
+        "step_bytes": step_bytes,
+        "splits": splits,
+        "sum_L": int(L1.sum()),
+        "c": c,
+    }
+    # flushed (cold L2/MALL) decode-only time
+    fl = Flusher(torch)
+    med, _ = time_op(torch, decode, 10, fl)
+    res["decode_us_flushed_median"] = med
+    del fl
+    return res
+
+
+# ---------------------------------------------------------------- extras ----
+def run_config1(torch, kvhp):
+    hq, hkv, d, max_seq = 32, 8, 64, 512
+    g = torch.Generator(device="cuda").manual_seed(1)
+    kc = torch.randn((hkv, max_seq, d), generator=g, device="cuda").half()
+    vc = torch.randn((hkv, max_seq, d), generator=g, device="cuda").half()
+    kn = torch.randn((1, hkv, d), generator=g, device="cuda").half()
+    vn = torch.randn((1, hkv, d), generator=g, device="cuda").half()
+    q = torch.randn((1, hq, d), generator=g, device="cuda").half()
+    out = torch.empty((1, hq, d), dtype=torch.float16, device="cuda")
+
+    def step():
+        kvhp.append_kv(kn, vn, kc, vc, 1, 511, hkv, max_seq, d)
+        kvhp.decode_gqa(q, kc, vc, out, 512, hq, hkv, max_seq, d)
+
+    for _ in range(10):
+        step()
+    warm_med, _ = time_op(torch, step, 50)
+    fl = Flusher(torch)
+    cold_med, _ = time_op(torch, step, 20, fl)
+    return {"workload": "config1: append 1 token at pos 511 + decode ctx 512, 32/8 heads, D=64",
+            "us_per_step_flushed": round(cold_med, 2), "us_per_step_warm": round(warm_med, 2),
+            "bytes": decode_bytes([512], hq, hkv, d) + append_bytes(1, hkv, d)}
+
+
+def run_config2(torch, kvhp):
+    hq, hkv, d = 32, 8, 128
+    fl = Flusher(torch)
+    rows = []
+    for L in (4096, 16384, 65536):
+        g = torch.Generator(device="cuda").manual_seed(L)
+        kc = torch.randn((1, hkv, L, d), generator=g, device="cuda").half()
+        vc = torch.randn((1, hkv, L, d), generator=g, device="cuda").half()
+        q = torch.randn((1, hq, d), generator=g, device="cuda").half()
+        out = torch.empty((1, hq, d), dtype=torch.float16, device="cuda")
+        lens = torch.tensor([L], dtype=torch.int32, device="cuda")
+        kv = kvhp.strided_view(kc, hkv * L * d, L * d, d)
+        vv = kvhp.strided_view(vc, hkv * L * d, L * d, d)
+        nb = decode_bytes([L], hq, hkv, d)
+        for s in (1, 4, 16, 64, 0):
+            ws_b = kvhp.decode_workspace_bytes(1, hq, hkv, d, L, s)
+            ws = torch.empty(max(ws_b, 256), dtype=torch.uint8, device="cuda")
+            kvhp.decode_workspace_init(ws)
+
+            def fn():
+                kvhp.decode_attention(q, kv, vv, lens, out, hq, hkv, d, L, s, ws)
+
+            for _ in range(3):
+                fn()
+            med, _ = time_op(torch, fn, 15, fl)
+            rows.append({"ctx": L, "splits": s if s else f"auto({kvhp.decode_auto_splits(1, hkv, d, L)})",
+                         "us": round(med, 2), "GB/s": round(nb / med / 1e3, 1),
+                         "pct_hbm": round(nb / med / 1e3 / HBM_PEAK_GBS * 100, 1)})
+        del kc, vc
+    return {"workload": "config2: B=1, 32/8 heads, D=128, contiguous fp16 KV, flushed", "rows": rows}
+
+
+def run_config4(torch, kvhp):
+    hq, hkv, d = 32, 8, 128
+    rows = []
+    fl = Flusher(torch)
+    for s in (512, 2048, 8192):
+        g = torch.Generator(device="cuda").manual_seed(s)
+        q = torch.randn((s, hq, d), generator=g, device="cuda").half()
+        k = torch.randn((s, hkv, d), generator=g, device="cuda").half()
+        v = torch.randn((s, hkv, d), generator=g, device="cuda").half()
+        out = torch.empty_like(q)
+
+        def fn():
+            kvhp.flash_prefill(q, k, v, out, s, hq, hkv, d, 1)
+
+        for _ in range(3):
+            fn()
+        med, _ = time_op(torch, fn, 10, fl)
+        flops = 2.0 * d * hq * s * (s + 1)
+        tf = flops / med / 1e6
+        rows.append({"S": s, "us": round(med, 2), "TFLOP/s": round(tf, 1),
+                     "pct_fp16_peak": round(tf / FP16_PEAK_TFLOPS * 100, 2)})
+    return {"workload": "config4: causal prefill B=1, 32/8 heads, D=128, fp16 in / fp32 acc",
+            "rows": rows}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+    import kvhp
+    kvhp.load()
+    assert torch.cuda.is_available(), "bench needs a GPU"
+    log("config3 timed steps ...")
+    r = run_config3(torch, kvhp, args)
+    c = r.pop("c")
+    dbytes = r["decode_bytes"]
+    achieved = dbytes / r["decode_us_mean"] / 1e3
+    line = {
+        "metric": METRIC,
+        "value": round(r["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 5),
+        "us_per_step": round(r["ms_per_step"] * 1e3, 2),
+        "pct_of_hbm_peak": round(r["value"] / HBM_PEAK_GBS * 100, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic N(0,1) fp16, seeded (torch generator 3; lengths numpy seed 3)",
+        "config": {
+            "workload": "BASELINE config 3: batched paged decode step, B=32, L~U[128,8192] "
+                        "(seed 3), 32 q / 8 KV heads, D=128, 16-token pages, random-permutation "
+                        "block tables; step = paged append 1 token/seq + split-K decode",
+            "sum_L": r["sum_L"], "splits": r["splits"], "decode_bytes": dbytes,
+            "step_bytes": r["step_bytes"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode_splitk_kernel<128,4,true>",
+                     "avg_launch_us": round(r["decode_us_mean"], 2),
+                     "flushed_launch_us": round(r["decode_us_flushed_median"], 2)},
+    }
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        line["cpu_baseline"] = cpu_baseline_config3(c, torch)
+    del c
+    torch.cuda.empty_cache()
+    extra = {}
+    parts = set(args.only.split(",")) if args.only else {"c1", "c2", "c4"}
+    if not args.no_extra:
+        if "c1" in parts:
+            log("config1 ...")
+            extra["config1"] = run_config1(torch, kvhp)
+        if "c2" in parts:
+            log("config2 ...")
+            extra["config2"] = run_config2(torch, kvhp)
+        if "c4" in parts:
+            log("config4 ...")
+            extra["config4"] = run_config4(torch, kvhp)
+    line["extra"] = extra
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

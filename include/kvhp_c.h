@@ -1,0 +1,167 @@
+/*
+ * kvhp_c.h -- C ABI of the MI355X (gfx950) KV-cache hot path.
+ *
+ * This is the drop-in boundary for the serving-engine KV-cache/attention
+ * path.  Each entry point names the reference interface it replaces
+ * (path:line in the reference tree).  The C++ mirror of the reference API
+ * (engine::KVCache, engine::cuda::append_kv_cache, decode_gqa_split, ...)
+ * lives in serving-engine_amd/engine/ and calls only these functions.
+ *
+ * Conventions (kept from the reference, src/cuda/kernels.h and
+ * src/runtime/kv_cache.h):
+ *   - every tensor argument is a raw device pointer the caller owns;
+ *     fp16 tensors are IEEE binary16 (passed as void*), indices int32;
+ *   - work is enqueued on `stream` (a hipStream_t; NULL = default stream)
+ *     and never synchronised;
+ *   - empty work (zero tokens / zero length) is a no-op returning KVHP_OK.
+ * Differences:
+ *   - errors are returned as a status code (< 0) instead of a C++ throw; the
+ *     message is available from kvhp_last_error() (thread-local).  The C++
+ *     mirror turns a non-zero status into std::runtime_error as the
+ *     reference's CUDA_CHECK did (src/common/cuda_utils.h:12-21).
+ *   - decode with seq_len <= 0 writes zeros (the reference leaves the output
+ *     untouched, src/cuda/decode_attention_split.cu:45-46).
+ */
+#ifndef KVHP_C_H
+#define KVHP_C_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVHP_OK 0
+#define KVHP_ERR_INVALID (-1)     /* bad shape / pointer / stride argument  */
+#define KVHP_ERR_UNSUPPORTED (-2) /* valid but not implemented (e.g. D>256) */
+#define KVHP_ERR_WORKSPACE (-3)   /* caller workspace too small             */
+#define KVHP_ERR_HIP (-4)         /* HIP runtime error (launch / alloc)     */
+
+#define KVHP_PAGE_SIZE 16         /* tokens per KV page                      */
+
+/* Strided or paged view of one K or V cache, the reference KVView
+ * (src/cuda/kv_view.h:17-31) extended with the block table its comment
+ * plans for (kv_view.h:9-10).
+ *   block_table == NULL (strided):
+ *     elem(b,h,s,d) = data[b*stride_b + h*stride_h + s*stride_s + d*stride_d]
+ *   block_table != NULL (paged; pool laid out [Hkv][num_pages][16][D]):
+ *     elem(b,h,s,d) = data[h*stride_h
+ *                         + (block_table[b*max_pages + s/16]*16 + s%16)*stride_s
+ *                         + d*stride_d]
+ *   Attention kernels require stride_d == 1 and 16-byte aligned rows. */
+typedef struct kvhp_kv_view {
+    const void* data;
+    int64_t stride_b;
+    int64_t stride_h;
+    int64_t stride_s;
+    int64_t stride_d;
+    const int32_t* block_table;
+    int32_t max_pages;   /* block-table row length (pages per sequence)       */
+    int32_t page_size;   /* must be KVHP_PAGE_SIZE in paged mode              */
+    int32_t num_pages;   /* pool capacity; page ids are clamped into range   */
+    int32_t reserved;
+} kvhp_kv_view;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* kvhp_last_error(void);
+/* ABI version of this library (KVHP_ABI_VERSION). */
+int kvhp_abi_version(void);
+#define KVHP_ABI_VERSION 1
+
+/* Replaces engine::cuda::append_kv_cache (src/runtime/kv_cache.h:80-91,
+ * kernel src/runtime/kv_cache.cu:8-61).  src [num_tokens][Hkv][D] token-major
+ * -> dst head base [Hkv][max_seq][D] at positions start_pos.., positions
+ * >= max_seq dropped.  Bit-exact copy. */
+int kvhp_append_kv(const void* src_k, const void* src_v, void* dst_k_head_base,
+                   void* dst_v_head_base, int num_tokens, int start_pos,
+                   int num_kv_heads, int max_seq, int head_dim, void* stream);
+
+/* Paged form of append_kv_cache (paging planned at src/cuda/kv_view.h:9-10,
+ * never built in the reference).  src [batch][num_tokens][Hkv][D]; token
+ * (b,t) goes to position start_pos[b]+t (start_pos: device int32[batch]) of
+ * pool [Hkv][num_pages][16][D] through block_tables [batch][max_pages].
+ * Dropped: pos < 0, pos/16 >= max_pages, page id outside [0,num_pages). */
+int kvhp_paged_append_kv(const void* src_k, const void* src_v, void* pool_k,
+                         void* pool_v, const int32_t* block_tables,
+                         int max_pages, const int32_t* start_pos, int batch,
+                         int num_tokens, int num_kv_heads, int head_dim,
+                         int num_pages, void* stream);
+
+/* Paged gather (the address map of KVView::get_ptr, src/cuda/kv_view.h:24-30,
+ * made explicit): out [batch][Hkv][max_len][D] <- pool through the block
+ * table for s < seq_lens[b]; other positions are written as zero. */
+int kvhp_paged_gather_kv(const void* pool_k, const void* pool_v,
+                         const int32_t* block_tables, int max_pages,
+                         const int32_t* seq_lens, int batch, int num_kv_heads,
+                         int head_dim, int num_pages, int max_len, void* out_k,
+                         void* out_v, void* stream);
+
+/* Split count the decode entry points choose when num_splits == 0. */
+int kvhp_decode_auto_splits(int batch, int num_kv_heads, int head_dim,
+                            int max_seq_len);
+/* Bytes of workspace kvhp_decode_attention needs for these arguments
+ * (num_splits == 0 -> auto).  Includes the split-merge ticket counters. */
+size_t kvhp_decode_workspace_bytes(int batch, int num_q_heads,
+                                   int num_kv_heads, int head_dim,
+                                   int max_seq_len, int num_splits);
+/* Zero the ticket counters of a fresh caller workspace (enqueued on stream).
+ * Every decode call leaves them zero again. */
+int kvhp_decode_workspace_init(void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/* Replaces engine::cuda::decode_gqa_split (src/cuda/kernels.h:117-133,
+ * src/cuda/decode_attention_split.cu:183-214), with the split-K partials and
+ * cross-split log-sum-exp merge the reference sizes but never runs
+ * (forward_gpu.cu:100, docs/reports/P7.md:13,32-34).
+ *   q [batch][Hq][D] fp16, seq_lens device int32[batch] (keys 0..len-1),
+ *   out [batch][Hq][D] fp16, kv_head = q_head / (Hq/Hkv),
+ *   scale 1/sqrt(D) (decode_attention_split.cu:197).
+ * num_splits: 0 = auto, else the number of KV chunks max_seq_len is cut into.
+ * workspace: NULL = library-owned per-device buffer (allocated on first use,
+ * so not capturable into a HIP graph); otherwise at least
+ * kvhp_decode_workspace_bytes() bytes prepared by kvhp_decode_workspace_init.
+ * Concurrent calls sharing one workspace race. */
+int kvhp_decode_attention(const void* q, const kvhp_kv_view* k_view,
+                          const kvhp_kv_view* v_view, const int32_t* seq_lens,
+                          void* out, int batch, int num_q_heads,
+                          int num_kv_heads, int head_dim, int max_seq_len,
+                          int num_splits, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* Replaces engine::cuda::decode_gqa (src/cuda/kernels.h:104-115,
+ * src/cuda/decode_attention.cu:114-137): one sequence, head-major cache
+ * [Hkv][max_seq][D], total_seq_len keys; routed to kvhp_decode_attention. */
+int kvhp_decode_gqa(const void* q, const void* k_cache, const void* v_cache,
+                    void* out, int total_seq_len, int num_q_heads,
+                    int num_kv_heads, int max_seq, int head_dim, void* stream);
+
+/* Replaces engine::cuda::flash_prefill_gqa (src/cuda/kernels.h:135-147,
+ * src/cuda/flash_prefill.cu:214-240): causal attention over token-major
+ * q [batch][S][Hq][D], k/v [batch][S][Hkv][D] -> out [batch][S][Hq][D]. */
+int kvhp_flash_prefill(const void* q, const void* k, const void* v, void* out,
+                       int64_t seq_len, int num_q_heads, int num_kv_heads,
+                       int head_dim, int batch, void* stream);
+
+/* flash_prefill_gqa that also writes each sequence's K/V rows into the paged
+ * pool as it consumes them (the reference does this with a separate
+ * append_kv_cache before attention, src/model/forward_gpu.cu:423-440).
+ * Positions 0..S-1 of sequence b go through block_tables[b]. */
+int kvhp_flash_prefill_paged(const void* q, const void* k, const void* v,
+                             void* out, int64_t seq_len, int num_q_heads,
+                             int num_kv_heads, int head_dim, int batch,
+                             void* pool_k, void* pool_v,
+                             const int32_t* block_tables, int max_pages,
+                             int num_pages, void* stream);
+
+/* Replaces engine::cuda::causal_gqa (src/cuda/kernels.h:71-87,
+ * src/cuda/causal_attention.cu:131-143): batch-1 causal attention; routed to
+ * the flash prefill kernel. */
+int kvhp_causal_gqa(const void* q, const void* k, const void* v, void* out,
+                    int64_t seq_len, int64_t num_q_heads, int64_t num_kv_heads,
+                    int64_t head_dim, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KVHP_C_H */

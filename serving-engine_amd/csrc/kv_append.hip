@@ -1,0 +1,242 @@
+// kv_append.hip -- KV-cache writes and the paged gather (bit-exact copies).
+//
+// Layout: every kernel moves 16-byte vectors (8 fp16).  One work item is one
+// 16-byte chunk of a K row plus the same chunk of the V row, so a wave copies
+// 1 KiB of K and 1 KiB of V per step with fully coalesced, 16-byte aligned
+// accesses; the token-major source [T][Hkv][D] is read in address order.
+// These kernels are HBM-bound byte copies: algorithmic traffic is exactly
+// 2 (read+write) x 2 (K,V) x T*Hkv*D*2 bytes (+4 B per block-table lookup).
+// A scalar (2-byte) variant handles head dims that are not multiples of 8.
+#include "kvhp_internal.h"
+
+namespace kvhp {
+
+namespace {
+
+constexpr int kCopyThreads = 256;
+
+// Contiguous append, same index map as the reference append_kv_kernel
+// (src/runtime/kv_cache.cu:20-35): src (t*Hkv + h)*D + d ->
+// dst (h*max_seq + start_pos + t)*D + d, positions >= max_seq skipped (:26).
+template <int VEC>
+__global__ void __launch_bounds__(kCopyThreads)
+append_contig_kernel(const f16* __restrict__ src_k, const f16* __restrict__ src_v,
+                     f16* __restrict__ dst_k, f16* __restrict__ dst_v,
+                     int64_t n_chunks, int chunks_per_row, int num_kv_heads,
+                     int start_pos, int max_seq, int head_dim) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_chunks;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / chunks_per_row;          // t*Hkv + h
+        const int c = static_cast<int>(i - row * chunks_per_row);
+        const int t = static_cast<int>(row / num_kv_heads);
+        const int h = static_cast<int>(row - (int64_t)t * num_kv_heads);
+        const int pos = start_pos + t;
+        if (pos < 0 || pos >= max_seq) continue;
+        const int64_t so = row * head_dim + (int64_t)c * VEC;
+        const int64_t dofs = ((int64_t)h * max_seq + pos) * head_dim + (int64_t)c * VEC;
+        if constexpr (VEC == 8) {
+            store_half8(dst_k + dofs, load_half8(src_k + so));
+            store_half8(dst_v + dofs, load_half8(src_v + so));
+        } else {
+            dst_k[dofs] = src_k[so];
+            dst_v[dofs] = src_v[so];
+        }
+    }
+}
+
+// Paged append: token (b,t) at position start_pos[b]+t lands in
+// pool[h][bt[b][pos/16]][pos%16][:].
+template <int VEC>
+__global__ void __launch_bounds__(kCopyThreads)
+append_paged_kernel(const f16* __restrict__ src_k, const f16* __restrict__ src_v,
+                    f16* __restrict__ pool_k, f16* __restrict__ pool_v,
+                    const int32_t* __restrict__ block_tables, int max_pages,
+                    const int32_t* __restrict__ start_pos, int64_t n_chunks,
+                    int chunks_per_row, int num_tokens, int num_kv_heads,
+                    int head_dim, int num_pages) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_chunks;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / chunks_per_row;          // (b*T + t)*Hkv + h
+        const int c = static_cast<int>(i - row * chunks_per_row);
+        const int64_t bt_row = row / num_kv_heads;       // b*T + t
+        const int h = static_cast<int>(row - bt_row * num_kv_heads);
+        const int b = static_cast<int>(bt_row / num_tokens);
+        const int t = static_cast<int>(bt_row - (int64_t)b * num_tokens);
+        const int pos = start_pos[b] + t;
+        if (pos < 0) continue;
+        const int pi = pos / kPage;
+        if (pi >= max_pages) continue;
+        const int pid = block_tables[(int64_t)b * max_pages + pi];
+        if (pid < 0 || pid >= num_pages) continue;
+        const int64_t so = row * head_dim + (int64_t)c * VEC;
+        const int64_t dofs =
+            (((int64_t)h * num_pages + pid) * kPage + (pos % kPage)) * head_dim +
+            (int64_t)c * VEC;
+        if constexpr (VEC == 8) {
+            store_half8(pool_k + dofs, load_half8(src_k + so));
+            store_half8(pool_v + dofs, load_half8(src_v + so));
+        } else {
+            pool_k[dofs] = src_k[so];
+            pool_v[dofs] = src_v[so];
+        }
+    }
+}
+
+// Paged gather: out[b][h][s][:] = pool[h][bt[b][s/16]][s%16][:] for
+// s < seq_lens[b], zero elsewhere (and for ids outside the pool).
+template <int VEC>
+__global__ void __launch_bounds__(kCopyThreads)
+gather_paged_kernel(const f16* __restrict__ pool_k, const f16* __restrict__ pool_v,
+                    const int32_t* __restrict__ block_tables, int max_pages,
+                    const int32_t* __restrict__ seq_lens, int64_t n_chunks,
+                    int chunks_per_row, int max_len, int num_kv_heads,
+                    int head_dim, int num_pages, f16* __restrict__ out_k,
+                    f16* __restrict__ out_v) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_chunks;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / chunks_per_row;          // (b*Hkv + h)*max_len + s
+        const int c = static_cast<int>(i - row * chunks_per_row);
+        const int64_t bh = row / max_len;
+        const int s = static_cast<int>(row - bh * max_len);
+        const int b = static_cast<int>(bh / num_kv_heads);
+        const int h = static_cast<int>(bh - (int64_t)b * num_kv_heads);
+        const int64_t o = row * head_dim + (int64_t)c * VEC;
+        int pid = -1;
+        if (s < seq_lens[b] && s / kPage < max_pages)
+            pid = block_tables[(int64_t)b * max_pages + s / kPage];
+        if (pid < 0 || pid >= num_pages) {
+            if constexpr (VEC == 8) {
+                const half8 z = {};
+                store_half8(out_k + o, z);
+                store_half8(out_v + o, z);
+            } else {
+                out_k[o] = f16(0);
+                out_v[o] = f16(0);
+            }
+            continue;
+        }
+        const int64_t src =
+            (((int64_t)h * num_pages + pid) * kPage + (s % kPage)) * head_dim +
+            (int64_t)c * VEC;
+        if constexpr (VEC == 8) {
+            store_half8(out_k + o, load_half8(pool_k + src));
+            store_half8(out_v + o, load_half8(pool_v + src));
+        } else {
+            out_k[o] = pool_k[src];
+            out_v[o] = pool_v[src];
+        }
+    }
+}
+
+// Grid for a grid-stride copy: enough waves to cover HBM latency on 256 CUs,
+// capped so very large copies loop instead of launching millions of groups.
+inline unsigned copy_grid(int64_t n_items) {
+    int64_t blocks = (n_items + kCopyThreads - 1) / kCopyThreads;
+    const int64_t cap = 256 * 32;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    return static_cast<unsigned>(blocks);
+}
+
+}  // namespace
+
+}  // namespace kvhp
+
+using namespace kvhp;
+
+extern "C" int kvhp_append_kv(const void* src_k, const void* src_v,
+                              void* dst_k_head_base, void* dst_v_head_base,
+                              int num_tokens, int start_pos, int num_kv_heads,
+                              int max_seq, int head_dim, void* stream) {
+    clear_error();
+    if (num_tokens <= 0) return KVHP_OK;  // kv_cache.cu:50
+    KVHP_REQUIRE(src_k && src_v && dst_k_head_base && dst_v_head_base,
+                 KVHP_ERR_INVALID, "append_kv: null pointer");
+    KVHP_REQUIRE(num_kv_heads > 0 && head_dim > 0 && max_seq > 0 && start_pos >= 0,
+                 KVHP_ERR_INVALID,
+                 "append_kv: bad shape (Hkv=%d D=%d max_seq=%d start=%d)",
+                 num_kv_heads, head_dim, max_seq, start_pos);
+    const bool vec = head_dim % 8 == 0 && aligned16(src_k) && aligned16(src_v) &&
+                     aligned16(dst_k_head_base) && aligned16(dst_v_head_base);
+    const int vw = vec ? 8 : 1;
+    const int cpr = head_dim / vw;
+    const int64_t n = (int64_t)num_tokens * num_kv_heads * cpr;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (vec)
+        hipLaunchKernelGGL(append_contig_kernel<8>, dim3(copy_grid(n)), dim3(kCopyThreads),
+                           0, s, (const f16*)src_k, (const f16*)src_v,
+                           (f16*)dst_k_head_base, (f16*)dst_v_head_base, n, cpr,
+                           num_kv_heads, start_pos, max_seq, head_dim);
+    else
+        hipLaunchKernelGGL(append_contig_kernel<1>, dim3(copy_grid(n)), dim3(kCopyThreads),
+                           0, s, (const f16*)src_k, (const f16*)src_v,
+                           (f16*)dst_k_head_base, (f16*)dst_v_head_base, n, cpr,
+                           num_kv_heads, start_pos, max_seq, head_dim);
+    return check_launch("append_kv");
+}
+
+extern "C" int kvhp_paged_append_kv(const void* src_k, const void* src_v,
+                                    void* pool_k, void* pool_v,
+                                    const int32_t* block_tables, int max_pages,
+                                    const int32_t* start_pos, int batch,
+                                    int num_tokens, int num_kv_heads,
+                                    int head_dim, int num_pages, void* stream) {
+    clear_error();
+    if (num_tokens <= 0 || batch <= 0) return KVHP_OK;
+    KVHP_REQUIRE(src_k && src_v && pool_k && pool_v && block_tables && start_pos,
+                 KVHP_ERR_INVALID, "paged_append_kv: null pointer");
+    KVHP_REQUIRE(num_kv_heads > 0 && head_dim > 0 && max_pages > 0 && num_pages > 0,
+                 KVHP_ERR_INVALID,
+                 "paged_append_kv: bad shape (Hkv=%d D=%d max_pages=%d pages=%d)",
+                 num_kv_heads, head_dim, max_pages, num_pages);
+    const bool vec = head_dim % 8 == 0 && aligned16(src_k) && aligned16(src_v) &&
+                     aligned16(pool_k) && aligned16(pool_v);
+    const int vw = vec ? 8 : 1;
+    const int cpr = head_dim / vw;
+    const int64_t n = (int64_t)batch * num_tokens * num_kv_heads * cpr;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (vec)
+        hipLaunchKernelGGL(append_paged_kernel<8>, dim3(copy_grid(n)), dim3(kCopyThreads),
+                           0, s, (const f16*)src_k, (const f16*)src_v, (f16*)pool_k,
+                           (f16*)pool_v, block_tables, max_pages, start_pos, n, cpr,
+                           num_tokens, num_kv_heads, head_dim, num_pages);
+    else
+        hipLaunchKernelGGL(append_paged_kernel<1>, dim3(copy_grid(n)), dim3(kCopyThreads),
+                           0, s, (const f16*)src_k, (const f16*)src_v, (f16*)pool_k,
+                           (f16*)pool_v, block_tables, max_pages, start_pos, n, cpr,
+                           num_tokens, num_kv_heads, head_dim, num_pages);
+    return check_launch("paged_append_kv");
+}
+
+extern "C" int kvhp_paged_gather_kv(const void* pool_k, const void* pool_v,
+                                    const int32_t* block_tables, int max_pages,
+                                    const int32_t* seq_lens, int batch,
+                                    int num_kv_heads, int head_dim,
+                                    int num_pages, int max_len, void* out_k,
+                                    void* out_v, void* stream) {
+    clear_error();
+    if (batch <= 0 || max_len <= 0) return KVHP_OK;
+    KVHP_REQUIRE(pool_k && pool_v && block_tables && seq_lens && out_k && out_v,
+                 KVHP_ERR_INVALID, "paged_gather_kv: null pointer");
+    KVHP_REQUIRE(num_kv_heads > 0 && head_dim > 0 && max_pages > 0 && num_pages > 0,
+                 KVHP_ERR_INVALID,
+                 "paged_gather_kv: bad shape (Hkv=%d D=%d max_pages=%d pages=%d)",
+                 num_kv_heads, head_dim, max_pages, num_pages);
+    const bool vec = head_dim % 8 == 0 && aligned16(pool_k) && aligned16(pool_v) &&
+                     aligned16(out_k) && aligned16(out_v);
+    const int vw = vec ? 8 : 1;
+    const int cpr = head_dim / vw;
+    const int64_t n = (int64_t)batch * num_kv_heads * max_len * cpr;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (vec)
+        hipLaunchKernelGGL(gather_paged_kernel<8>, dim3(copy_grid(n)), dim3(kCopyThreads),
+                           0, s, (const f16*)pool_k, (const f16*)pool_v, block_tables,
+                           max_pages, seq_lens, n, cpr, max_len, num_kv_heads,
+                           head_dim, num_pages, (f16*)out_k, (f16*)out_v);
+    else
+        hipLaunchKernelGGL(gather_paged_kernel<1>, dim3(copy_grid(n)), dim3(kCopyThreads),
+                           0, s, (const f16*)pool_k, (const f16*)pool_v, block_tables,
+                           max_pages, seq_lens, n, cpr, max_len, num_kv_heads,
+                           head_dim, num_pages, (f16*)out_k, (f16*)out_v);
+    return check_launch("paged_gather_kv");
+}

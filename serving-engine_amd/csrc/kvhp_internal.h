@@ -1,0 +1,106 @@
+// kvhp_internal.h -- shared definitions of the gfx950 KV-cache hot-path library.
+//
+// Device side: 16-bit float vector types, 16-byte load/store helpers, wave64
+// DPP reductions.  Host side: thread-local error reporting and HIP error
+// plumbing for the C ABI in include/kvhp_c.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "kvhp_c.h"
+
+namespace kvhp {
+
+typedef _Float16 f16;
+typedef f16 half8 __attribute__((ext_vector_type(8)));
+typedef f16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kPage = KVHP_PAGE_SIZE;
+
+// ---------------------------------------------------------------- host ----
+void set_error(const char* fmt, ...);
+void clear_error();
+int fail(int code, const char* fmt, ...);
+// Report the launch status of the kernels just enqueued.
+int check_launch(const char* what);
+
+#define KVHP_REQUIRE(cond, code, ...)          \
+    do {                                       \
+        if (!(cond)) return ::kvhp::fail(code, __VA_ARGS__); \
+    } while (0)
+
+#define KVHP_HIP(call, what)                                                  \
+    do {                                                                      \
+        hipError_t e_ = (call);                                               \
+        if (e_ != hipSuccess)                                                 \
+            return ::kvhp::fail(KVHP_ERR_HIP, "%s: %s", what,                 \
+                                hipGetErrorString(e_));                       \
+    } while (0)
+
+inline bool aligned16(const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// -------------------------------------------------------------- device ----
+// Wave64 DPP row (16-lane) butterflies.  Controls: quad_perm [1,0,3,2] = 0xB1,
+// quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                           0xF, 0xF, false));
+}
+
+// Max over the 16 lanes of each DPP row; every lane of the row gets it.
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f32<0xB1>(x));
+    x = fmaxf(x, dpp_f32<0x4E>(x));
+    x = fmaxf(x, dpp_f32<0x141>(x));
+    x = fmaxf(x, dpp_f32<0x140>(x));
+    return x;
+}
+
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f32<0xB1>(x);
+    x += dpp_f32<0x4E>(x);
+    x += dpp_f32<0x141>(x);
+    x += dpp_f32<0x140>(x);
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+    x = row16_max(x);
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+    x = row16_sum(x);
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
+
+__device__ __forceinline__ half8 load_half8(const f16* p) {
+    return *reinterpret_cast<const half8*>(p);
+}
+
+__device__ __forceinline__ void store_half8(f16* p, half8 v) {
+    *reinterpret_cast<half8*>(p) = v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+    return __builtin_amdgcn_exp2f(x);
+}
+
+}  // namespace kvhp

@@ -1,0 +1,225 @@
+"""ctypes binding of libkvhp.so, the gfx950 KV-cache hot-path library.
+
+The C ABI is declared in include/kvhp_c.h; this module mirrors it one to one
+for Python callers (tests, bench, smoke).  Device memory and streams come from
+torch: every tensor argument is a torch tensor on the GPU, every `stream` is a
+torch.cuda.Stream (default: the current stream).  Errors raise KVHPError with
+the library's kvhp_last_error() message, the Python counterpart of the
+std::runtime_error the reference's CUDA_CHECK throws
+(src/common/cuda_utils.h:12-21).
+
+There is no CPU fallback: if the library is missing, load() raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libkvhp.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "kvhp_c.h")
+
+PAGE_SIZE = 16
+KVHP_OK = 0
+KVHP_ERR_INVALID = -1
+KVHP_ERR_UNSUPPORTED = -2
+KVHP_ERR_WORKSPACE = -3
+KVHP_ERR_HIP = -4
+
+
+class KVHPError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"kvhp error {code}: {msg}")
+        self.code = code
+
+
+class KVView(ctypes.Structure):
+    """kvhp_kv_view: strided (block_table == NULL) or paged view of K or V."""
+
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("stride_b", ctypes.c_int64),
+        ("stride_h", ctypes.c_int64),
+        ("stride_s", ctypes.c_int64),
+        ("stride_d", ctypes.c_int64),
+        ("block_table", ctypes.c_void_p),
+        ("max_pages", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "kvhp_last_error": (ctypes.c_char_p, []),
+    "kvhp_abi_version": (_i32, []),
+    "kvhp_append_kv": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "kvhp_paged_append_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32,
+                                    _i32, _i32, _vp]),
+    "kvhp_paged_gather_kv": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32,
+                                    _vp, _vp, _vp]),
+    "kvhp_decode_auto_splits": (_i32, [_i32, _i32, _i32, _i32]),
+    "kvhp_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "kvhp_decode_workspace_init": (_i32, [_vp, _sz, _vp]),
+    "kvhp_decode_attention": (_i32, [_vp, ctypes.POINTER(KVView), ctypes.POINTER(KVView), _vp,
+                                     _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "kvhp_decode_gqa": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "kvhp_flash_prefill": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
+    "kvhp_flash_prefill_paged": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp,
+                                        _vp, _vp, _i32, _i32, _vp]),
+    "kvhp_causal_gqa": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libkvhp.so (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> list:
+    return list(_SIGNATURES)
+
+
+def last_error() -> str:
+    return load().kvhp_last_error().decode()
+
+
+def _check(rc: int) -> None:
+    if rc != KVHP_OK:
+        raise KVHPError(rc, last_error())
+
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+# ----------------------------------------------------------------- views --
+def strided_view(t, stride_b: int, stride_h: int, stride_s: int, stride_d: int = 1) -> KVView:
+    v = KVView()
+    v.data = t.data_ptr()
+    v.stride_b, v.stride_h, v.stride_s, v.stride_d = stride_b, stride_h, stride_s, stride_d
+    v.block_table = None
+    v.max_pages = v.page_size = v.num_pages = 0
+    return v
+
+
+def paged_view(pool, block_tables) -> KVView:
+    """View over a pool [Hkv][P][16][D] with int32 block tables [B][max_pages]."""
+    hkv, p, page, d = pool.shape
+    assert page == PAGE_SIZE
+    v = KVView()
+    v.data = pool.data_ptr()
+    v.stride_b = 0
+    v.stride_h = p * page * d
+    v.stride_s = d
+    v.stride_d = 1
+    v.block_table = block_tables.data_ptr()
+    v.max_pages = block_tables.shape[1]
+    v.page_size = page
+    v.num_pages = p
+    return v
+
+
+# ------------------------------------------------------------- entry pts --
+def append_kv(src_k, src_v, dst_k, dst_v, num_tokens, start_pos, num_kv_heads, max_seq,
+              head_dim, stream=None):
+    _check(load().kvhp_append_kv(_ptr(src_k), _ptr(src_v), _ptr(dst_k), _ptr(dst_v),
+                                 num_tokens, start_pos, num_kv_heads, max_seq, head_dim,
+                                 _stream(stream)))
+
+
+def paged_append_kv(src_k, src_v, pool_k, pool_v, block_tables, start_pos, batch, num_tokens,
+                    num_kv_heads, head_dim, stream=None):
+    _check(load().kvhp_paged_append_kv(
+        _ptr(src_k), _ptr(src_v), _ptr(pool_k), _ptr(pool_v), _ptr(block_tables),
+        block_tables.shape[1], _ptr(start_pos), batch, num_tokens, num_kv_heads, head_dim,
+        pool_k.shape[1], _stream(stream)))
+
+
+def paged_gather_kv(pool_k, pool_v, block_tables, seq_lens, max_len, out_k, out_v,
+                    stream=None):
+    hkv, p, _, d = pool_k.shape
+    _check(load().kvhp_paged_gather_kv(
+        _ptr(pool_k), _ptr(pool_v), _ptr(block_tables), block_tables.shape[1], _ptr(seq_lens),
+        seq_lens.shape[0], hkv, d, p, max_len, _ptr(out_k), _ptr(out_v), _stream(stream)))
+
+
+def decode_auto_splits(batch, num_kv_heads, head_dim, max_seq_len) -> int:
+    return load().kvhp_decode_auto_splits(batch, num_kv_heads, head_dim, max_seq_len)
+
+
+def decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
+                           num_splits=0) -> int:
+    return load().kvhp_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim,
+                                              max_seq_len, num_splits)
+
+
+def decode_workspace_init(ws, stream=None):
+    _check(load().kvhp_decode_workspace_init(_ptr(ws), ws.numel() * ws.element_size(),
+                                             _stream(stream)))
+
+
+def decode_attention(q, k_view: KVView, v_view: KVView, seq_lens, out, num_q_heads,
+                     num_kv_heads, head_dim, max_seq_len, num_splits=0, workspace=None,
+                     stream=None):
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(load().kvhp_decode_attention(
+        _ptr(q), ctypes.byref(k_view), ctypes.byref(v_view), _ptr(seq_lens), _ptr(out),
+        seq_lens.shape[0], num_q_heads, num_kv_heads, head_dim, max_seq_len, num_splits,
+        _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+def decode_gqa(q, k_cache, v_cache, out, total_seq_len, num_q_heads, num_kv_heads, max_seq,
+               head_dim, stream=None):
+    _check(load().kvhp_decode_gqa(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                                  total_seq_len, num_q_heads, num_kv_heads, max_seq, head_dim,
+                                  _stream(stream)))
+
+
+def flash_prefill(q, k, v, out, seq_len, num_q_heads, num_kv_heads, head_dim, batch=1,
+                  stream=None):
+    _check(load().kvhp_flash_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(out), seq_len,
+                                     num_q_heads, num_kv_heads, head_dim, batch,
+                                     _stream(stream)))
+
+
+def flash_prefill_paged(q, k, v, out, seq_len, num_q_heads, num_kv_heads, head_dim, batch,
+                        pool_k, pool_v, block_tables, stream=None):
+    _check(load().kvhp_flash_prefill_paged(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), seq_len, num_q_heads, num_kv_heads, head_dim,
+        batch, _ptr(pool_k), _ptr(pool_v), _ptr(block_tables), block_tables.shape[1],
+        pool_k.shape[1], _stream(stream)))
+
+
+def causal_gqa(q, k, v, out, seq_len, num_q_heads, num_kv_heads, head_dim, stream=None):
+    _check(load().kvhp_causal_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(out), seq_len, num_q_heads,
+                                  num_kv_heads, head_dim, _stream(stream)))

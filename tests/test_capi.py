@@ -1,0 +1,117 @@
+"""CPU-side checks of the C ABI: the library loads, exports every function
+include/kvhp_c.h declares, and rejects bad arguments on the host before any
+GPU work (no compute calls here)."""
+import ctypes
+import re
+
+import pytest
+
+import kvhp
+
+
+def _declared_functions():
+    text = open(kvhp.HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kvhp_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_surface():
+    declared = _declared_functions()
+    assert declared == sorted(kvhp.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    lib = kvhp.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.kvhp_abi_version() == 1
+
+
+def test_kv_view_struct_layout_matches_header():
+    # 1 pointer + 4 int64 strides + pointer + 4 int32 = 64 bytes
+    assert ctypes.sizeof(kvhp.KVView) == 64
+
+
+def test_auto_split_policy():
+    # page-aligned chunks of >= 64 tokens, never more than 1024 splits
+    assert kvhp.decode_auto_splits(1, 8, 128, 64) == 1
+    for b, hkv, L in [(1, 8, 512), (1, 8, 4096), (1, 8, 65536), (32, 8, 8192), (1, 4, 2176)]:
+        s = kvhp.decode_auto_splits(b, hkv, 128, L)
+        assert 1 <= s <= 1024
+        chunk = -(-L // s)
+        assert s <= -(-L // 64)
+        assert b * hkv * s >= min(4096, b * hkv * -(-L // 64)) // 2 or chunk <= 128
+
+
+def test_workspace_sizing():
+    # no workspace when a single split covers the sequence
+    assert kvhp.decode_workspace_bytes(1, 32, 8, 128, 64, 1) == 0
+    n = kvhp.decode_workspace_bytes(2, 32, 8, 128, 4096, 16)
+    # tickets (2*8 u32) + partial o (2*32*16*128 f32) + (m,l) pairs, 256-B aligned
+    assert n >= 2 * 32 * 16 * (128 + 2) * 4 + 2 * 8 * 4
+    assert n % 256 == 0
+
+
+def _null_view():
+    return kvhp.KVView()
+
+
+def test_host_validation_errors():
+    lib = kvhp.load()
+    v = kvhp.KVView()
+    v.data = 0x1000
+    v.stride_d = 1
+    # group size not integral
+    rc = lib.kvhp_decode_attention(ctypes.c_void_p(0x1000), ctypes.byref(v), ctypes.byref(v),
+                                   ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000), 1, 6, 4, 64,
+                                   128, 0, None, 0, None)
+    assert rc == kvhp.KVHP_ERR_INVALID and "multiple" in kvhp.last_error()
+    # head_dim beyond 256
+    rc = lib.kvhp_decode_attention(ctypes.c_void_p(0x1000), ctypes.byref(v), ctypes.byref(v),
+                                   ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000), 1, 8, 4, 512,
+                                   128, 0, None, 0, None)
+    assert rc == kvhp.KVHP_ERR_UNSUPPORTED
+    # null view data
+    nv = _null_view()
+    rc = lib.kvhp_decode_attention(ctypes.c_void_p(0x1000), ctypes.byref(nv), ctypes.byref(v),
+                                   ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000), 1, 8, 4, 64,
+                                   128, 0, None, 0, None)
+    assert rc == kvhp.KVHP_ERR_INVALID
+    # mixed paged / strided views
+    pv = kvhp.KVView()
+    pv.data = 0x1000
+    pv.stride_d = 1
+    pv.block_table = 0x2000
+    pv.max_pages, pv.page_size, pv.num_pages = 4, 16, 4
+    rc = lib.kvhp_decode_attention(ctypes.c_void_p(0x1000), ctypes.byref(pv), ctypes.byref(v),
+                                   ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000), 1, 8, 4, 64,
+                                   128, 0, None, 0, None)
+    assert rc == kvhp.KVHP_ERR_INVALID and "paged" in kvhp.last_error()
+    # caller workspace too small for 16 splits
+    rc = lib.kvhp_decode_attention(ctypes.c_void_p(0x1000), ctypes.byref(v), ctypes.byref(v),
+                                   ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000), 1, 8, 4, 64,
+                                   4096, 16, ctypes.c_void_p(0x3000), 64, None)
+    assert rc == kvhp.KVHP_ERR_WORKSPACE
+    # append / prefill argument checks
+    rc = lib.kvhp_append_kv(None, None, None, None, 4, 0, 2, 16, 64, None)
+    assert rc == kvhp.KVHP_ERR_INVALID
+    assert lib.kvhp_append_kv(None, None, None, None, 0, 0, 2, 16, 64, None) == kvhp.KVHP_OK
+    rc = lib.kvhp_paged_append_kv(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                  ctypes.c_void_p(16), ctypes.c_void_p(16), 0,
+                                  ctypes.c_void_p(16), 1, 1, 2, 64, 4, None)
+    assert rc == kvhp.KVHP_ERR_INVALID
+    rc = lib.kvhp_flash_prefill(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                ctypes.c_void_p(16), 8, 7, 2, 64, 1, None)
+    assert rc == kvhp.KVHP_ERR_INVALID
+    rc = lib.kvhp_flash_prefill_paged(ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                      ctypes.c_void_p(16), ctypes.c_void_p(16), 8, 8, 2, 64, 1,
+                                      None, None, None, 1, 1, None)
+    assert rc == kvhp.KVHP_ERR_INVALID
+    # zero-length work is a no-op, as in the reference
+    assert lib.kvhp_decode_gqa(None, None, None, None, 0, 8, 2, 16, 64, None) == kvhp.KVHP_OK
+    assert lib.kvhp_causal_gqa(None, None, None, None, 0, 8, 2, 64, None) == kvhp.KVHP_OK
+
+
+def test_error_raises_in_binding():
+    with pytest.raises(kvhp.KVHPError):
+        kvhp._check(kvhp.load().kvhp_append_kv(None, None, None, None, 4, 0, 2, 16, 64, None))

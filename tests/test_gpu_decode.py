@@ -1,0 +1,230 @@
+"""GPU parity of split-K decode attention against the oracle, through the C ABI.
+
+Tolerance: max-abs 2e-3 / max-rel 1e-2 (see gpu_util.assert_attn_close).
+"""
+import numpy as np
+import pytest
+
+import kvhp
+import oracle
+from gpu_util import (assert_attn_close, contiguous_from_tokens, from_gpu, make_block_tables,
+                      note, sync, to_gpu, to_gpu_f16, uniform_f16)
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_contig(q, kc, vc, lens, hq, hkv, d, cap, splits=0, workspace=None):
+    """q [B][Hq][D], kc/vc [B][Hkv][cap][D] (fp16 numpy) -> GPU output fp32."""
+    import torch
+    b = q.shape[0]
+    kt, vt = to_gpu_f16(kc), to_gpu_f16(vc)
+    kview = kvhp.strided_view(kt, hkv * cap * d, cap * d, d)
+    vview = kvhp.strided_view(vt, hkv * cap * d, cap * d, d)
+    out = torch.full((b, hq, d), float("nan"), dtype=torch.float16, device="cuda")
+    kvhp.decode_attention(to_gpu_f16(q), kview, vview, to_gpu(np.asarray(lens, np.int32)), out,
+                          hq, hkv, d, cap, splits, workspace)
+    sync()
+    return from_gpu(out).astype(np.float32)
+
+
+def test_decode_reference_shapes():
+    """tests/test_attention.cpp:34-175: 25 shapes, B 1..3, Hkv=2, G 7 or 1..7,
+    D=64, lengths {1, 17, 513, rand<=600}, U(-1,1) inputs."""
+    rng = np.random.default_rng(701)
+    for i in range(25):
+        b = 1 if i % 4 == 0 else int(rng.integers(1, 4))
+        hkv = 2
+        g = 7 if i % 3 == 0 else int(rng.integers(1, 8))
+        hq, d = hkv * g, 64
+        lens = np.array([1 if i == 0 else 17 if i == 1 else 513 if i == 2
+                         else int(rng.integers(1, 601)) for _ in range(b)], np.int32)
+        cap = int(lens.max())
+        q = uniform_f16(rng, (b, hq, d))
+        kc, vc = uniform_f16(rng, (b, hkv, cap, d)), uniform_f16(rng, (b, hkv, cap, d))
+        note(f"decode ref case {i}: B={b} G={g} lens={lens.tolist()}")
+        got = _run_contig(q, kc, vc, lens, hq, hkv, d, cap)
+        ref = oracle.decode_attention(q.astype(np.float32), kc.astype(np.float32),
+                                      vc.astype(np.float32), lens, hq, hkv, d)
+        assert_attn_close(got, ref, f"case {i}")
+
+
+@pytest.mark.parametrize("L", [1, 15, 16, 63, 64, 65, 1000, 4096])
+@pytest.mark.parametrize("splits", [1, 4, 16, 64, 0])
+def test_decode_d128_splits(L, splits):
+    """32 q / 8 KV heads, D=128 at ragged lengths and
+    every split count of the config-2 sweep; N(0,1) inputs."""
+    rng = np.random.default_rng(1000 + L)
+    hq, hkv, d = 32, 8, 128
+    q = oracle.normal_f16(rng, (1, hq, d))
+    kc, vc = oracle.normal_f16(rng, (1, hkv, L, d)), oracle.normal_f16(rng, (1, hkv, L, d))
+    note(f"decode d128 L={L} splits={splits}")
+    got = _run_contig(q, kc, vc, [L], hq, hkv, d, L, splits)
+    ref = oracle.decode_attention(q.astype(np.float32), kc.astype(np.float32),
+                                  vc.astype(np.float32), np.array([L], np.int32), hq, hkv, d,
+                                  nthreads=8)
+    assert_attn_close(got, ref, f"L={L} splits={splits}")
+
+
+def test_config1_append_then_decode():
+    """B=1, 32/8 heads, D=64, 511 cached tokens, append one
+    K/V row at position 511 with the append kernel, then decode over 512."""
+    import torch
+    rng = np.random.default_rng(1)
+    hq, hkv, d, max_seq = 32, 8, 64, 512
+    kc = np.zeros((hkv, max_seq, d), np.float16)
+    vc = np.zeros_like(kc)
+    kc[:, :511] = oracle.normal_f16(rng, (hkv, 511, d))
+    vc[:, :511] = oracle.normal_f16(rng, (hkv, 511, d))
+    knew, vnew = oracle.normal_f16(rng, (1, hkv, d)), oracle.normal_f16(rng, (1, hkv, d))
+    q = oracle.normal_f16(rng, (1, hq, d))
+    kt, vt = to_gpu_f16(kc), to_gpu_f16(vc)
+    note("config1 append + decode")
+    kvhp.append_kv(to_gpu_f16(knew), to_gpu_f16(vnew), kt, vt, 1, 511, hkv, max_seq, d)
+    out = torch.empty((1, hq, d), dtype=torch.float16, device="cuda")
+    kvhp.decode_gqa(to_gpu_f16(q), kt, vt, out, 512, hq, hkv, max_seq, d)
+    sync()
+    kc[:, 511], vc[:, 511] = knew[0], vnew[0]
+    assert np.array_equal(from_gpu(kt), kc)
+    ref = oracle.decode_attention(q.astype(np.float32), kc[None].astype(np.float32),
+                                  vc[None].astype(np.float32), np.array([512], np.int32),
+                                  hq, hkv, d)
+    assert_attn_close(from_gpu(out).astype(np.float32), ref, "config1")
+
+
+def test_config2_64k_split_sweep_and_invariance():
+    """BASELINE config 2 at its largest context (65536) with splits
+    {1,4,16,64}: every split count matches the oracle, and the outputs of
+    different split counts agree with each other."""
+    rng = np.random.default_rng(2)
+    hq, hkv, d, L = 32, 8, 128, 65536
+    q = oracle.normal_f16(rng, (1, hq, d))
+    kc, vc = oracle.normal_f16(rng, (1, hkv, L, d)), oracle.normal_f16(rng, (1, hkv, L, d))
+    ref = oracle.decode_attention(q.astype(np.float32), kc.astype(np.float32),
+                                  vc.astype(np.float32), np.array([L], np.int32), hq, hkv, d,
+                                  nthreads=8)
+    outs = []
+    for s in (1, 4, 16, 64):
+        note(f"config2 L=65536 splits={s}")
+        got = _run_contig(q, kc, vc, [L], hq, hkv, d, L, s)
+        assert_attn_close(got, ref, f"splits={s}")
+        outs.append(got)
+    for o in outs[1:]:
+        assert np.max(np.abs(o - outs[0])) <= 2e-3
+
+
+def _paged_case(rng, b, lens, hq, hkv, d, with_append):
+    """Builds a paged pool from token-major K/V through the oracle's paged
+    append (host), returns GPU output and oracle reference."""
+    import torch
+    lens = np.asarray(lens, np.int32)
+    bt, P = make_block_tables(rng, lens + 1)
+    T = int(lens.max()) + 1
+    tk = oracle.normal_f16(rng, (b, T, hkv, d))
+    tv = oracle.normal_f16(rng, (b, T, hkv, d))
+    q = oracle.normal_f16(rng, (b, hq, d))
+    pk = np.zeros((hkv, P, 16, d), np.uint16)
+    pv = np.zeros_like(pk)
+    for i in range(b):
+        n = int(lens[i]) if with_append else int(lens[i]) + 1
+        oracle.paged_append(tk[i:i + 1, :n].view(np.uint16), tv[i:i + 1, :n].view(np.uint16),
+                            pk, pv, bt[i:i + 1], np.array([0], np.int32), 1, n, hkv, d)
+    pk_t = to_gpu(pk.view(np.float16))
+    pv_t = to_gpu(pv.view(np.float16))
+    bt_t = to_gpu(bt)
+    if with_append:   # the step's new token goes in with the GPU append kernel
+        newk = np.ascontiguousarray(tk[np.arange(b), lens])[:, None]
+        newv = np.ascontiguousarray(tv[np.arange(b), lens])[:, None]
+        kvhp.paged_append_kv(to_gpu_f16(newk), to_gpu_f16(newv), pk_t, pv_t, bt_t,
+                             to_gpu(lens), b, 1, hkv, d)
+    L1 = lens + 1
+    out = torch.empty((b, hq, d), dtype=torch.float16, device="cuda")
+    kvhp.decode_attention(to_gpu_f16(q), kvhp.paged_view(pk_t, bt_t), kvhp.paged_view(pv_t, bt_t),
+                          to_gpu(L1), out, hq, hkv, d, int(L1.max()))
+    sync()
+    kc = contiguous_from_tokens(tk.astype(np.float32), L1, int(L1.max()))
+    vc = contiguous_from_tokens(tv.astype(np.float32), L1, int(L1.max()))
+    ref = oracle.decode_attention(q.astype(np.float32), kc, vc, L1, hq, hkv, d, nthreads=8)
+    return from_gpu(out).astype(np.float32), ref
+
+
+@pytest.mark.parametrize("b,maxlen,hq,hkv,d", [(8, 1500, 32, 8, 128), (5, 300, 14, 2, 64),
+                                               (3, 900, 32, 4, 64), (4, 200, 16, 1, 128)])
+def test_paged_decode_with_append(b, maxlen, hq, hkv, d):
+    rng = np.random.default_rng(b * 31 + maxlen)
+    lens = rng.integers(0, maxlen, size=b)
+    note(f"paged decode B={b} Hq={hq} Hkv={hkv} D={d} lens={lens.tolist()}")
+    got, ref = _paged_case(rng, b, lens, hq, hkv, d, with_append=True)
+    assert_attn_close(got, ref, "paged")
+
+
+def test_config3_paged_decode_full_size():
+    """BASELINE config 3 at full size: 32 sequences with seeded lengths in
+    [128, 8192], 32/8 heads, D=128, 16-token pages on a seeded random
+    permutation; one appended token per sequence, then decode."""
+    rng = np.random.default_rng(3)
+    lens = rng.integers(128, 8193, size=32) - 1   # + the appended token
+    note(f"config3 full: sum L={int(lens.sum()) + 32}")
+    got, ref = _paged_case(rng, 32, lens, 32, 8, 128, with_append=True)
+    assert_attn_close(got, ref, "config3")
+
+
+@pytest.mark.parametrize("d", [16, 32, 48, 64])
+def test_decode_gqa_legacy_api(d):
+    """tests/test_kv_cache.cpp:98-196: single sequence over a head-major
+    [Hkv][max_seq][D] cache, D in {16..64}, ctx <= 64, G 1..5, Hkv 1..3."""
+    import torch
+    rng = np.random.default_rng(102 + d)
+    for i in range(6):
+        L = 1 if i == 0 else int(rng.integers(1, 65))
+        max_seq = L + int(rng.integers(0, 32))
+        hkv = int(rng.integers(1, 4))
+        hq = hkv * int(rng.integers(1, 6))
+        q = uniform_f16(rng, (1, hq, d))
+        kc, vc = uniform_f16(rng, (hkv, max_seq, d)), uniform_f16(rng, (hkv, max_seq, d))
+        out = torch.empty((hq, d), dtype=torch.float16, device="cuda")
+        note(f"decode_gqa D={d} case {i}: L={L} Hq={hq} Hkv={hkv}")
+        kvhp.decode_gqa(to_gpu_f16(q), to_gpu_f16(kc), to_gpu_f16(vc), out, L, hq, hkv,
+                        max_seq, d)
+        sync()
+        ref = oracle.decode_attention(q.astype(np.float32), kc[None].astype(np.float32),
+                                      vc[None].astype(np.float32), np.array([L], np.int32),
+                                      hq, hkv, d)
+        assert_attn_close(from_gpu(out)[None].astype(np.float32), ref, f"D={d} case {i}")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(24, 2, 128), (8, 8, 96), (12, 4, 256)])
+def test_decode_generic_shapes(hq, hkv, d):
+    """Shapes outside the MFMA kernel's template set (G=12, D=96, D=256) run
+    on the generic kernel with the same results contract."""
+    rng = np.random.default_rng(hq + d)
+    lens = np.array([1, 77, 300], np.int32)
+    cap = 300
+    q = oracle.normal_f16(rng, (3, hq, d))
+    kc, vc = oracle.normal_f16(rng, (3, hkv, cap, d)), oracle.normal_f16(rng, (3, hkv, cap, d))
+    note(f"decode generic Hq={hq} Hkv={hkv} D={d}")
+    got = _run_contig(q, kc, vc, lens, hq, hkv, d, cap)
+    ref = oracle.decode_attention(q.astype(np.float32), kc.astype(np.float32),
+                                  vc.astype(np.float32), lens, hq, hkv, d)
+    assert_attn_close(got, ref, "generic")
+
+
+def test_decode_caller_workspace_reuse_and_empty_sequences():
+    """A caller workspace is prepared once; consecutive calls (the second
+    smaller) leave its ticket counters clean; zero-length sequences write 0."""
+    import torch
+    rng = np.random.default_rng(4)
+    hq, hkv, d, cap = 32, 8, 128, 3000
+    ws_bytes = kvhp.decode_workspace_bytes(4, hq, hkv, d, cap, 32)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    kvhp.decode_workspace_init(ws)
+    for lens in ([3000, 0, 1234, 65], [100, 7, 0]):
+        b = len(lens)
+        q = oracle.normal_f16(rng, (b, hq, d))
+        kc, vc = oracle.normal_f16(rng, (b, hkv, cap, d)), oracle.normal_f16(rng, (b, hkv, cap, d))
+        note(f"workspace reuse lens={lens}")
+        got = _run_contig(q, kc, vc, lens, hq, hkv, d, cap, 32, ws)
+        ref = oracle.decode_attention(q.astype(np.float32), kc.astype(np.float32),
+                                      vc.astype(np.float32), np.array(lens, np.int32), hq, hkv, d)
+        assert_attn_close(got, ref, f"lens={lens}")
+        ticket_bytes = 256
+        assert int(torch.count_nonzero(ws[:ticket_bytes])) == 0

@@ -1,0 +1,138 @@
+"""GPU parity of causal flash prefill against the oracle's restatement of the
+reference cpu::causal_gqa (src/cpu/ops.cpp:223-284), through the C ABI.
+
+Tolerance: max-abs 2e-3 / max-rel 1e-2 (see gpu_util.assert_attn_close).
+Long prompts are checked on a seeded sample of rows (rows are independent, so
+each sampled row is an exact per-row check), always including the first and
+last rows and the 64-row block edges.
+"""
+import numpy as np
+import pytest
+
+import kvhp
+import oracle
+from gpu_util import (assert_attn_close, from_gpu, make_block_tables, note, sync, to_gpu,
+                      to_gpu_f16, uniform_f16)
+
+pytestmark = pytest.mark.gpu
+
+
+def _prefill(q, k, v, hq, hkv, d, batch=1):
+    import torch
+    s = q.shape[-3]
+    out = torch.full(q.shape, float("nan"), dtype=torch.float16, device="cuda")
+    kvhp.flash_prefill(to_gpu_f16(q), to_gpu_f16(k), to_gpu_f16(v), out, s, hq, hkv, d, batch)
+    sync()
+    return from_gpu(out).astype(np.float32)
+
+
+def test_prefill_reference_shapes():
+    """tests/test_attention.cpp:180-291: 25 shapes, Hkv=2, G 7 or 1..7, D=64,
+    S in {1, 15, 17, 65, rand<=120}, U(-1,1) inputs."""
+    rng = np.random.default_rng(702)
+    for i in range(25):
+        g = 7 if i % 3 == 0 else int(rng.integers(1, 8))
+        hkv, d = 2, 64
+        hq = hkv * g
+        s = [1, 15, 17, 65][i] if i < 4 else int(rng.integers(1, 121))
+        q = uniform_f16(rng, (s, hq, d))
+        k, v = uniform_f16(rng, (s, hkv, d)), uniform_f16(rng, (s, hkv, d))
+        note(f"prefill ref case {i}: S={s} G={g}")
+        got = _prefill(q, k, v, hq, hkv, d)
+        ref = oracle.causal_gqa(q.astype(np.float32), k.astype(np.float32),
+                                v.astype(np.float32), hq, hkv, d, nthreads=8)
+        assert_attn_close(got, ref, f"case {i}")
+
+
+@pytest.mark.parametrize("s", [1, 2, 63, 64, 65, 200, 512])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (32, 4, 64)])
+def test_prefill_baseline_heads_full_check(s, hq, hkv, d):
+    rng = np.random.default_rng(s * 13 + d)
+    q = oracle.normal_f16(rng, (s, hq, d))
+    k, v = oracle.normal_f16(rng, (s, hkv, d)), oracle.normal_f16(rng, (s, hkv, d))
+    note(f"prefill S={s} Hq={hq} Hkv={hkv} D={d}")
+    got = _prefill(q, k, v, hq, hkv, d)
+    ref = oracle.causal_gqa(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32),
+                            hq, hkv, d, nthreads=8)
+    assert_attn_close(got, ref, f"S={s}")
+
+
+def _sample_rows(rng, s, n=24):
+    fixed = {0, 1, 2, 63, 64, 65, 127, 128, s // 2, s - 2, s - 1}
+    rows = set(r for r in fixed if 0 <= r < s)
+    rows |= set(int(x) for x in rng.integers(0, s, size=n))
+    return sorted(rows)
+
+
+@pytest.mark.parametrize("s", [2048, 8192])
+def test_prefill_config4_sampled_rows(s):
+    """BASELINE config 4 (32/8 heads, D=128, N(0,1)) at S=2048 and 8192; every
+    head of a seeded row sample is checked against the oracle."""
+    rng = np.random.default_rng(4 + s)
+    hq, hkv, d = 32, 8, 128
+    q = oracle.normal_f16(rng, (s, hq, d))
+    k, v = oracle.normal_f16(rng, (s, hkv, d)), oracle.normal_f16(rng, (s, hkv, d))
+    note(f"prefill config4 S={s}")
+    got = _prefill(q, k, v, hq, hkv, d)
+    qf, kf, vf = q.astype(np.float32), k.astype(np.float32), v.astype(np.float32)
+    for r in _sample_rows(rng, s):
+        ref = oracle.causal_gqa(qf, kf, vf, hq, hkv, d, rows=(r, r + 1), nthreads=8)
+        assert_attn_close(got[r], ref[r], f"S={s} row {r}")
+
+
+def test_prefill_batched():
+    rng = np.random.default_rng(77)
+    b, s, hq, hkv, d = 3, 150, 16, 4, 128
+    q = oracle.normal_f16(rng, (b, s, hq, d))
+    k, v = oracle.normal_f16(rng, (b, s, hkv, d)), oracle.normal_f16(rng, (b, s, hkv, d))
+    note("prefill batched B=3")
+    got = _prefill(q, k, v, hq, hkv, d, batch=b)
+    for i in range(b):
+        ref = oracle.causal_gqa(q[i].astype(np.float32), k[i].astype(np.float32),
+                                v[i].astype(np.float32), hq, hkv, d, nthreads=8)
+        assert_attn_close(got[i], ref, f"batch {i}")
+
+
+@pytest.mark.parametrize("s,hq,hkv,d", [(2048, 32, 8, 128), (333, 14, 2, 64), (70, 6, 3, 96)])
+def test_prefill_paged_writes_pages_bit_exact(s, hq, hkv, d):
+    """flash_prefill_paged writes K/V rows into the pages exactly as the paged
+    append does (config 4: K/V written into 16-token pages as produced)."""
+    import torch
+    rng = np.random.default_rng(s + d)
+    q = oracle.normal_f16(rng, (s, hq, d))
+    k, v = oracle.normal_f16(rng, (s, hkv, d)), oracle.normal_f16(rng, (s, hkv, d))
+    bt, P = make_block_tables(rng, [s])
+    pool0 = oracle.normal_f16(rng, (hkv, P, 16, d))
+    pk, pv = to_gpu_f16(pool0), to_gpu_f16(pool0.copy())
+    out = torch.empty((s, hq, d), dtype=torch.float16, device="cuda")
+    note(f"prefill paged S={s} Hq={hq} D={d}")
+    kvhp.flash_prefill_paged(to_gpu_f16(q), to_gpu_f16(k), to_gpu_f16(v), out, s, hq, hkv, d,
+                             1, pk, pv, to_gpu(bt))
+    sync()
+    ek = pool0.view(np.uint16).copy()
+    ev = pool0.view(np.uint16).copy()
+    oracle.paged_append(k[None].view(np.uint16), v[None].view(np.uint16), ek, ev, bt,
+                        np.array([0], np.int32), 1, s, hkv, d)
+    assert np.array_equal(from_gpu(pk).view(np.uint16), ek)
+    assert np.array_equal(from_gpu(pv).view(np.uint16), ev)
+    rows = _sample_rows(rng, s, 8)
+    got = from_gpu(out).astype(np.float32)
+    qf, kf, vf = q.astype(np.float32), k.astype(np.float32), v.astype(np.float32)
+    for r in rows:
+        ref = oracle.causal_gqa(qf, kf, vf, hq, hkv, d, rows=(r, r + 1), nthreads=8)
+        assert_attn_close(got[r], ref[r], f"row {r}")
+
+
+def test_causal_gqa_api_routes_to_prefill():
+    import torch
+    rng = np.random.default_rng(45)
+    s, hq, hkv, d = 90, 14, 2, 64
+    q = uniform_f16(rng, (s, hq, d))
+    k, v = uniform_f16(rng, (s, hkv, d)), uniform_f16(rng, (s, hkv, d))
+    out = torch.empty((s, hq, d), dtype=torch.float16, device="cuda")
+    note("causal_gqa api")
+    kvhp.causal_gqa(to_gpu_f16(q), to_gpu_f16(k), to_gpu_f16(v), out, s, hq, hkv, d)
+    sync()
+    ref = oracle.causal_gqa(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32),
+                            hq, hkv, d)
+    assert_attn_close(from_gpu(out).astype(np.float32), ref, "causal_gqa")
