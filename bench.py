@@ -17,7 +17,7 @@ oracle's restatement of the reference CPU attention arithmetic
 (oracle/kvhp_oracle.c) on the same inputs, on the host cores.
 
 Also reported under "extra" (each measured with L2+MALL flushed by a 1 GiB
-write before every rep unless labelled warm): config 1 (decode at ctx 512),
+read before every rep unless labelled warm): config 1 (decode at ctx 512),
 config 2 (ctx 4K/16K/64K x splits 1/4/16/64), config 4 (causal prefill
 S=512/2048/8192, TFLOP/s vs fp16 MFMA peak).
 """
@@ -50,17 +50,22 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 2 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4")
+    ap.add_argument("--profile", action="store_true",
+                    help="short run for rocprofv3: a 256 MiB device copy (counter "
+                         "calibration) then the config-3 steps; no CPU baseline, no extras")
     return ap.parse_args()
 
 
 class Flusher:
-    """Writes 1 GiB (4x the 256 MB MALL) to evict L2 and MALL between reps."""
+    """Reads 1 GiB (4x the 256 MB MALL) to evict L2 and MALL between reps.
+    A read leaves clean lines behind, so the timed kernel does not pay for
+    writing back the flush's own data."""
 
     def __init__(self, torch):
-        self.buf = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+        self.buf = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
 
     def __call__(self):
-        self.buf.zero_()
+        self.buf.sum()
 
 
 def time_op(torch, fn, reps, flush=None):
@@ -296,6 +301,21 @@ def run_config4(torch, kvhp):
             "rows": rows}
 
 
+def traffic_from_profile(dbytes):
+    """HBM bytes per decode call from the committed rocprofv3 --pmc summary
+    (profiles/decode_config3_traffic.json), if present."""
+    path = os.path.join(ROOT, "profiles", "decode_config3_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return {"bytes": t.get("hbm_bytes_per_call"), "fetch_bytes": t.get("fetch_bytes"),
+            "write_bytes": t.get("write_bytes"),
+            "ratio_to_algorithmic": round(t["hbm_bytes_per_call"] / dbytes, 4)
+            if t.get("hbm_bytes_per_call") else None,
+            "source": "profiles/decode_config3_traffic.json"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -306,6 +326,16 @@ def main():
     import kvhp
     kvhp.load()
     assert torch.cuda.is_available(), "bench needs a GPU"
+    if args.profile:
+        args.no_cpu = args.no_extra = True
+        # plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch
+        # calibrate the counters (256 MiB read + 256 MiB written)
+        src = torch.ones(1 << 26, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log("config3 timed steps ...")
     r = run_config3(torch, kvhp, args)
     c = r.pop("c")
@@ -333,10 +363,15 @@ def main():
             "sum_L": r["sum_L"], "splits": r["splits"], "decode_bytes": dbytes,
             "step_bytes": r["step_bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_splitk_kernel<128,4,true>",
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profile(dbytes),
+                     "kernel": "decode_splitk_kernel<128,4,true> + decode_merge_kernel<128,4>",
                      "avg_launch_us": round(r["decode_us_mean"], 2),
-                     "flushed_launch_us": round(r["decode_us_flushed_median"], 2)},
+                     "flushed_launch_us": round(r["decode_us_flushed_median"], 2),
+                     "flushed_GBps": round(dbytes / r["decode_us_flushed_median"] / 1e3, 1),
+                     "note": "achieved = algorithmic bytes / mean HIP-event time of the decode "
+                             "call in the timed loop (working set 504 MB vs 256 MB MALL); "
+                             "flushed = same call after a 1 GiB read"},
     }
     if not args.no_cpu:
         log("cpu baseline ...")

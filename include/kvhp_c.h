@@ -101,12 +101,13 @@ int kvhp_paged_gather_kv(const void* pool_k, const void* pool_v,
 int kvhp_decode_auto_splits(int batch, int num_kv_heads, int head_dim,
                             int max_seq_len);
 /* Bytes of workspace kvhp_decode_attention needs for these arguments
- * (num_splits == 0 -> auto).  Includes the split-merge ticket counters. */
+ * (num_splits == 0 -> auto): fp32 split partials (o[D], m, l) per
+ * (sequence, query head, split); 0 when one split covers max_seq_len. */
 size_t kvhp_decode_workspace_bytes(int batch, int num_q_heads,
                                    int num_kv_heads, int head_dim,
                                    int max_seq_len, int num_splits);
-/* Zero the ticket counters of a fresh caller workspace (enqueued on stream).
- * Every decode call leaves them zero again. */
+/* Zero a caller workspace (enqueued on stream).  Optional: the decode entry
+ * points never read workspace bytes they did not write in the same call. */
 int kvhp_decode_workspace_init(void* workspace, size_t workspace_bytes,
                                void* stream);
 
@@ -120,8 +121,9 @@ int kvhp_decode_workspace_init(void* workspace, size_t workspace_bytes,
  * num_splits: 0 = auto, else the number of KV chunks max_seq_len is cut into.
  * workspace: NULL = library-owned per-device buffer (allocated on first use,
  * so not capturable into a HIP graph); otherwise at least
- * kvhp_decode_workspace_bytes() bytes prepared by kvhp_decode_workspace_init.
- * Concurrent calls sharing one workspace race. */
+ * kvhp_decode_workspace_bytes() bytes.  With more than one split the call is
+ * two launches on `stream` (split kernel, then merge kernel).  Concurrent
+ * calls sharing one workspace race. */
 int kvhp_decode_attention(const void* q, const kvhp_kv_view* k_view,
                           const kvhp_kv_view* v_view, const int32_t* seq_lens,
                           void* out, int batch, int num_q_heads,

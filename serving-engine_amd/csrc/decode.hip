@@ -6,28 +6,28 @@
 // byte is read from HBM exactly once (the reference re-reads each KV row once
 // per query head, src/cuda/decode_attention_split.cu:40-49).
 //
-// Per 64-token iteration (4 pages of 16 tokens):
-//   QK^T  on MFMA: v_mfma_f32_16x16x32_f16 with B = K^T (lane l holds 16 B of
-//         token (page t, slot l%16) at dims 32c + 8(l/16)) and A = Q (row r
-//         holds head r % CG).  Accumulator tile t then holds, in lane l,
-//         scores of token (t, l%16) for heads 4(l/16)+e (mod CG); lane l keeps
-//         the tile that belongs to it, so the 64 lanes hold 64 tokens x CG
-//         heads with no redundancy.  K loads are 16 B per lane, 64 B
-//         contiguous per row, full 64 B sectors.
-//   softmax in fp32, log2 domain (scores pre-scaled by log2(e)/sqrt(D)),
-//         wave64 DPP row reductions + 2 cross-row swizzles for the running
-//         max; p and the rescale factors go through 2 KiB of LDS.
-//   PV    on VALU: lane l owns 8 dims of one token per V load (16 B, a wave
-//         load covers whole 256 B rows, 1 KiB contiguous), so V is read in
-//         address order; fp32 FMAs, one accumulator set per lane row.
-// Loads for iteration i+1 are issued while iteration i computes (K after the
-// QK MFMAs retire their operands, V after PV).
+// Per 64-token iteration (4 pages of 16 tokens), both contractions run on
+// v_mfma_f32_16x16x32_f16:
+//   S = Q K^T   A = Q (row r holds head r % CG), B = K^T loaded straight from
+//               HBM: lane l holds 16 B of token (page t, slot l%16) at dims
+//               32c + 8(l/16), i.e. 64 contiguous bytes per row.  Lane l keeps
+//               the tile that belongs to it, so the 64 lanes hold 64 tokens x 4
+//               heads each with no redundancy.
+//   softmax     fp32, log2 domain (scores pre-scaled by log2(e)/sqrt(D)); the
+//               running max per head is a DPP row reduction + 2 swizzles.  Each
+//               lane's heads are the same rows it owns in the O accumulator, so
+//               the rescale factor never leaves the lane.
+//   O += P V    A = P (fp16) and B = V^T, both read from this wave's LDS tiles
+//               with ds_read_b64_tr_b16 (transposing 8-byte reads); V arrives
+//               from HBM as whole 256 B rows (1 KiB per wave load) and is
+//               written to LDS row-major.
+// K and V live in a two-deep register ring: iteration i+2 is fetched while
+// iteration i computes, with identical loads on every path so the compiler
+// keeps exact vmcnt waits (no pipeline drain).
 //
-// Split merge: each non-final split stores (m, l, o[D]) in fp32; the
-// last-arriving workgroup of a (sequence, kv_head) -- found with a ticket
-// counter in the workspace -- merges by log-sum-exp and writes fp16 output,
-// so a decode is a single kernel launch.  Counters are returned to zero by
-// the merging workgroup.
+// Splits: a sequence whose keys fit one split gets its output written
+// directly; otherwise each split stores (m, l, o[D]) in fp32 and
+// decode_merge_kernel (a second, tiny launch) combines them by log-sum-exp.
 //
 // Roofline: HBM-bound; algorithmic bytes per (token, kv_head) are 4*D
 // (K + V fp16) plus the q read and output write per query head.
@@ -35,13 +35,15 @@
 
 #include <cmath>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace kvhp {
 
 namespace {
 
-constexpr int kMaxSplits = 1024;
+constexpr int kMaxSplits = 256;   // partials per (sequence, kv head)
+constexpr int kTok = 64;          // tokens per pipelined iteration (4 pages)
 
 struct KVDev {
     const f16* data;
@@ -59,11 +61,10 @@ struct DecodeArgs {
     f16* out;              // [B][Hq][D]
     float* ws_o;           // [B*Hq][nsplit][D]
     float* ws_ml;          // [B*Hq][nsplit][2]  (max in log2 units, sum)
-    uint32_t* tickets;     // [B*Hkv]
     int Hq, Hkv;
     int chunk;             // tokens per split, multiple of 64
     int nsplit;            // split slots in the workspace
-    int cap;               // tokens addressable per sequence (= nsplit*chunk)
+    int cap;               // tokens addressable per sequence
     int fixed_len;         // length of every sequence when seq_lens == nullptr
     float scale_log2;      // log2(e) / sqrt(D)
 };
@@ -72,36 +73,48 @@ __device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
     return a.seq_lens ? a.seq_lens[b] : a.fixed_len;
 }
 
-template <bool PAGED>
-__device__ __forceinline__ const f16* page_base(const f16* base, const int32_t* bt_row,
-                                                int64_t ss, int page_idx,
-                                                int num_pages) {
-    if constexpr (PAGED) {
-        int pid = bt_row[page_idx];
-        pid = pid < 0 ? 0 : (pid >= num_pages ? num_pages - 1 : pid);
-        return base + (int64_t)pid * kPage * ss;
-    } else {
-        return base + (int64_t)page_idx * kPage * ss;
-    }
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+typedef __attribute__((address_space(3))) f16 lds_f16;
+
+// ds_read_b64_tr_b16: within each 16-lane block, lane i receives element
+// (i % 4) of the 8-byte groups addressed by lanes 4k + i/4, k = 0..3.
+// So if lane j addresses the 4 consecutive elements [col0 + 4(j%4), +4) of
+// row R(j/4), lane i gets column col0 + i of rows R(0..3): a 4 x 16 tile
+// transposed into the MFMA operand layout.
+__device__ __forceinline__ short4v lds_read_tr16(const f16* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(lds_f16*)p);
 }
+
+__device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
+    return __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+template <int G>
+struct Groups {
+    static constexpr int CG = G <= 4 ? 4 : (G <= 8 ? 8 : 16);  // heads per MFMA row set
+    static constexpr int R = CG / 4;                             // lane head groups
+};
 
 template <int D, int G, bool PAGED>
 __global__ void __launch_bounds__(kWave)
 decode_splitk_kernel(const DecodeArgs a) {
-    constexpr int CG = G <= 4 ? 4 : (G <= 8 ? 8 : 16);  // heads per MFMA row set
-    constexpr int NC = D / 32;       // MFMA k-chunks over head_dim
+    constexpr int TOK = kTok;
+    constexpr int CG = Groups<G>::CG;
+    constexpr int R = Groups<G>::R;
+    constexpr int NC = D / 32;       // MFMA k-chunks of the QK contraction
+    constexpr int ND = D / 16;       // 16-dim blocks of the output
     constexpr int LPR = D / 8;       // lanes per V row (16 B each)
     constexpr int RPL = kWave / LPR; // V rows per wave load
-    constexpr int NVL = 64 / RPL;    // V loads per 64-token iteration
-    constexpr int R = CG / 4;        // score rounds (4 heads per lane each)
-    constexpr int TPR = 4 / R;       // 16-token tiles per round
-    constexpr int GQ = (G + 3) / 4;  // float4 groups of p read per token
+    constexpr int NVL = TOK / RPL;   // V loads per iteration
+    constexpr int NT = TOK / 16;     // 16-token pages per iteration
+    constexpr int TPR = 4 / R;       // tiles per score round
+    constexpr int NR = NT / TPR;     // score rounds per iteration
+    constexpr int VP = D + 16;       // V tile row pitch in halfs (bank skew)
+    constexpr int REP = 4 / R;       // lane groups holding the same heads
 
-    __shared__ floatx4 p_lds[2][64][CG / 4];
-    __shared__ float alpha_lds[2][CG];
-    __shared__ float m_lds[CG];
-    __shared__ float w_lds[kMaxSplits];
-    __shared__ uint32_t ticket_lds;
+    __shared__ __attribute__((aligned(16))) f16 v_lds[TOK * VP];
+    __shared__ __attribute__((aligned(16))) f16 p_lds[TOK * CG];
 
     const int lane = threadIdx.x;
     const int g = lane >> 4;
@@ -125,30 +138,27 @@ decode_splitk_kernel(const DecodeArgs a) {
     if (split >= nsb) return;
     const int t_begin = split * a.chunk;
     const int t_end = min(L, t_begin + a.chunk);
-    const int n_iter = (t_end - t_begin + 63) >> 6;
-    const int last_tok = L - 1;
+    const int n_iter = (t_end - t_begin + TOK - 1) / TOK;
+    // Loads never leave this split: rows past its end re-read its last row
+    // (a cache hit), so prefetches can be issued unconditionally.
+    const int last_tok = t_end - 1;
     const int last_pi = last_tok >> 4;
+    const int last_slot = last_tok & 15;
 
     const int64_t ssk = a.k.stride_s, ssv = a.v.stride_s;
     const f16* kbase;
     const f16* vbase;
-    const int32_t* btk = nullptr;
-    const int32_t* btv = nullptr;
+    const int32_t* bt = nullptr;
     if constexpr (PAGED) {
         kbase = a.k.data + kvh * a.k.stride_h;
         vbase = a.v.data + kvh * a.v.stride_h;
-        btk = a.k.bt + (int64_t)b * a.k.max_pages;
-        btv = a.v.bt + (int64_t)b * a.v.max_pages;
+        bt = a.k.bt + (int64_t)b * a.k.max_pages;  // K and V share one table
     } else {
         kbase = a.k.data + b * a.k.stride_b + kvh * a.k.stride_h;
         vbase = a.v.data + b * a.v.stride_b + kvh * a.v.stride_h;
     }
-    const f16* klast = page_base<PAGED>(kbase, btk, ssk, last_pi, a.k.num_pages) +
-                       (last_tok & 15) * ssk;
-    const f16* vlast = page_base<PAGED>(vbase, btv, ssv, last_pi, a.v.num_pages) +
-                       (last_tok & 15) * ssv;
 
-    // A operand: lane l holds q[head (l%16) % CG][dims 32c + 8(l/16) .. +8].
+    // A operand of QK: lane l holds q[head (l%16) % CG][dims 32c + 8(l/16) .. +8].
     half8 qa[NC];
     {
         const int hq = col % CG;
@@ -162,70 +172,87 @@ decode_splitk_kernel(const DecodeArgs a) {
         }
     }
 
-    half8 kreg[4][NC];
-    half8 vreg[NVL];
     const int vrow = lane / LPR;
     const int vdim = 8 * (lane % LPR);
 
-    auto load_k = [&](int T0) {
+    // Physical row offset (in units of rows) of each page of the iteration
+    // starting at T0; pages past the split clamp to its last page.  Uniform
+    // across the wave, so these are scalar loads.
+    auto page_rows = [&](int T0, int64_t (&pr)[NT]) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < NT; ++t) {
             const int pi = min((T0 >> 4) + t, last_pi);
-            const f16* pg = page_base<PAGED>(kbase, btk, ssk, pi, a.k.num_pages);
-            const int tok = T0 + 16 * t + col;
-            const f16* rp = (tok <= last_tok) ? pg + col * ssk : klast;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) kreg[t][c] = load_half8(rp + 32 * c + 8 * g);
+            if constexpr (PAGED) {
+                int pid = bt[pi];
+                pid = pid < 0 ? 0 : (pid >= a.k.num_pages ? a.k.num_pages - 1 : pid);
+                pr[t] = (int64_t)pid * kPage;
+            } else {
+                pr[t] = (int64_t)pi * kPage;
+            }
         }
     };
-    auto load_v = [&](int T0) {
+
+    half8 kbuf[2][NT][NC];
+    half8 vbuf[2][NVL];
+
+    auto load_k = [&](auto S_, int T0) {
+        constexpr int S = decltype(S_)::value;
+        int64_t pr[NT];
+        page_rows(T0, pr);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int slot = (T0 + 16 * t + col <= last_tok) ? col : last_slot;
+            const f16* rp = kbase + (pr[t] + slot) * ssk + 8 * g;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) kbuf[S][t][c] = load_half8(rp + 32 * c);
+        }
+    };
+    auto load_v = [&](auto S_, int T0) {
+        constexpr int S = decltype(S_)::value;
+        int64_t pr[NT];
+        page_rows(T0, pr);
 #pragma unroll
         for (int j = 0; j < NVL; ++j) {
             const int t = (RPL * j) >> 4;
-            const int slot = ((RPL * j) & 15) + vrow;
-            const int pi = min((T0 >> 4) + t, last_pi);
-            const f16* pg = page_base<PAGED>(vbase, btv, ssv, pi, a.v.num_pages);
-            const int tok = T0 + RPL * j + vrow;
-            const f16* rp = (tok <= last_tok) ? pg + slot * ssv : vlast;
-            vreg[j] = load_half8(rp + vdim);
+            const int s0 = ((RPL * j) & 15) + vrow;
+            const int slot = (T0 + RPL * j + vrow <= last_tok) ? s0 : last_slot;
+            vbuf[S][j] = load_half8(vbase + (pr[t] + slot) * ssv + vdim);
         }
     };
 
-    float m_run[4];
+    float m_run[4], l_part[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) m_run[e] = -1e30f;
-    float acc[G][8];
-    float lsum[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        lsum[h] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+    for (int e = 0; e < 4; ++e) {
+        m_run[e] = -1e30f;
+        l_part[e] = 0.f;
     }
-
-    load_k(t_begin);
-    load_v(t_begin);
-
-    for (int it = 0; it < n_iter; ++it) {
-        const int T0 = t_begin + 64 * it;
-        const int par = it & 1;
-
-        // ---- S = Q K^T on MFMA, one accumulator per 16-token tile.
-        floatx4 C[4];
+    floatx4 o[ND];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+    for (int db = 0; db < ND; ++db) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // One iteration on ring slot S.  With PREFETCH the slot is refilled with
+    // iteration it+2 as soon as each half is consumed.
+    auto step = [&](auto S_, auto PF_, int it) {
+        constexpr int S = decltype(S_)::value;
+        constexpr bool PREFETCH = decltype(PF_)::value;
+        const int T0 = t_begin + TOK * it;
+
+        // ---- S = Q K^T, one accumulator per 16-token page.
+        floatx4 C[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
             C[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c)
-                C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kreg[t][c], C[t], 0, 0, 0);
+                C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kbuf[S][t][c], C[t], 0, 0, 0);
         }
-        if (it + 1 < n_iter) load_k(T0 + 64);
+        if constexpr (PREFETCH) load_k(S_, T0 + 2 * TOK);
 
-        // ---- scores of the lane's own tokens (heads 4*(g%R)+e).
-        float s[R][4];
-        int tile_of[R];
+        // ---- the lane's own scores: heads 4*(g%R)+e of token 16*tile + col.
+        float s[NR][4];
+        int tile_of[NR];
 #pragma unroll
-        for (int rr = 0; rr < R; ++rr) {
+        for (int rr = 0; rr < NR; ++rr) {
             const int sub = g / R;
             floatx4 sel = C[rr * TPR];
 #pragma unroll
@@ -238,149 +265,208 @@ decode_splitk_kernel(const DecodeArgs a) {
             for (int e = 0; e < 4; ++e) s[rr][e] = ok ? sel[e] * a.scale_log2 : -INFINITY;
         }
 
-        // ---- running max per head over the wave, rescale factor.
+        // ---- running max per head, rescale factor (lane-local heads).
         float alpha[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float mt = s[0][e];
 #pragma unroll
-            for (int rr = 1; rr < R; ++rr) mt = fmaxf(mt, s[rr][e]);
+            for (int rr = 1; rr < NR; ++rr) mt = fmaxf(mt, s[rr][e]);
             mt = row16_max(mt);
             if constexpr (R == 1) mt = fmaxf(mt, __shfl_xor(mt, 16));
             if constexpr (R <= 2) mt = fmaxf(mt, __shfl_xor(mt, 32));
             const float mn = fmaxf(m_run[e], mt);
             alpha[e] = fast_exp2(m_run[e] - mn);
             m_run[e] = mn;
+            l_part[e] *= alpha[e];
         }
-#pragma unroll
-        for (int rr = 0; rr < R; ++rr) {
-            floatx4 pv;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) pv[e] = fast_exp2(s[rr][e] - m_run[e]);
-            p_lds[par][16 * tile_of[rr] + col][g % R] = pv;
-        }
-        if (col == 0 && g < R) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) alpha_lds[par][4 * g + e] = alpha[e];
-        }
-        __syncthreads();
 
-        // ---- O += P V on VALU in the V-row layout.
+        // ---- P (fp16) and V into this wave's LDS tiles.
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float al = alpha_lds[par][h];
-            lsum[h] *= al;
+        for (int rr = 0; rr < NR; ++rr) {
+            half4 ph;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] *= al;
+            for (int e = 0; e < 4; ++e) {
+                ph[e] = static_cast<f16>(fast_exp2(s[rr][e] - m_run[e]));
+                l_part[e] += static_cast<float>(ph[e]);
+            }
+            *reinterpret_cast<half4*>(&p_lds[(16 * tile_of[rr] + col) * CG + 4 * (g % R)]) = ph;
         }
 #pragma unroll
-        for (int j = 0; j < NVL; ++j) {
-            const int tok = RPL * j + vrow;
-            float pw[GQ * 4];
+        for (int j = 0; j < NVL; ++j)
+            *reinterpret_cast<half8*>(&v_lds[(RPL * j + vrow) * VP + vdim]) = vbuf[S][j];
+        if constexpr (PREFETCH) load_v(S_, T0 + 2 * TOK);
+
 #pragma unroll
-            for (int u = 0; u < GQ; ++u) {
-                const floatx4 t4 = p_lds[par][tok][u];
-                pw[4 * u + 0] = t4[0];
-                pw[4 * u + 1] = t4[1];
-                pw[4 * u + 2] = t4[2];
-                pw[4 * u + 3] = t4[3];
-            }
-            float vf[8];
+        for (int db = 0; db < ND; ++db)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vf[e] = static_cast<float>(vreg[j][e]);
+            for (int e = 0; e < 4; ++e) o[db][e] *= alpha[e];
+
+        // ---- O += P V: k-slot (g, e') of step ks is token ks*32 + 8g + e'.
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                lsum[h] += pw[h];
+        for (int ks = 0; ks < TOK / 32; ++ks) {
+            const int trow = ks * 32 + 8 * g + col / 4;
+            const f16* pa = &p_lds[trow * CG + 4 * ((col % 4) % R)];
+            const half8 pop = cat_half8(lds_read_tr16(pa), lds_read_tr16(pa + 4 * CG));
+            const f16* pv = &v_lds[trow * VP + 4 * (col % 4)];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pw[h], vf[e], acc[h][e]);
+            for (int db = 0; db < ND; ++db) {
+                const half8 vop = cat_half8(lds_read_tr16(pv + 16 * db),
+                                            lds_read_tr16(pv + 16 * db + 4 * VP));
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, vop, o[db], 0, 0, 0);
             }
         }
-        if (it + 1 < n_iter) load_v(T0 + 64);
+    };
+
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using Pf = std::true_type;
+    using NoPf = std::false_type;
+    load_k(I0{}, t_begin);
+    load_v(I0{}, t_begin);
+    load_k(I1{}, t_begin + TOK);
+    load_v(I1{}, t_begin + TOK);
+    int it = 0;
+    for (; it + 3 < n_iter; it += 2) {
+        step(I0{}, Pf{}, it);
+        step(I1{}, Pf{}, it + 1);
+    }
+    // tail: at most three iterations, no further prefetch past the split
+    if (it + 2 < n_iter) {
+        step(I0{}, Pf{}, it);
+        step(I1{}, NoPf{}, it + 1);
+        step(I0{}, NoPf{}, it + 2);
+    } else {
+        step(I0{}, NoPf{}, it);
+        if (it + 1 < n_iter) step(I1{}, NoPf{}, it + 1);
     }
 
-    // ---- combine the V-row partial sums (lanes with equal lane % LPR).
+    // ---- row sums over the lanes that share this lane's heads.
+    float l_tot[4];
 #pragma unroll
-    for (int off = LPR; off < kWave; off <<= 1) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            lsum[h] += __shfl_xor(lsum[h], off);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
-        }
+    for (int e = 0; e < 4; ++e) {
+        float x = row16_sum(l_part[e]);
+        if constexpr (R == 1) x += __shfl_xor(x, 16);
+        if constexpr (R <= 2) x += __shfl_xor(x, 32);
+        l_tot[e] = x;
     }
-    if (col == 0 && g < R) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) m_lds[4 * g + e] = m_run[e];
-    }
-    __syncthreads();
 
+    // Lane (g, col) holds O[head 4*(g%R)+e][dim 16*db + col]; the REP lane
+    // groups with equal g%R hold identical rows and split the stores by db.
+    const int hg = g % R;
+    const int rep = g / R;
     if (nsb == 1) {
-        if (lane < LPR) {
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float inv = lsum[h] > 0.f ? 1.f / lsum[h] : 0.f;
-                half8 o;
+        for (int e = 0; e < 4; ++e) {
+            const int h = 4 * hg + e;
+            if (h >= G) continue;
+            const float inv = l_tot[e] > 0.f ? 1.f / l_tot[e] : 0.f;
+            f16* orow = a.out + (row0 + h) * D;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = static_cast<f16>(acc[h][e] * inv);
-                store_half8(a.out + (row0 + h) * D + 8 * lane, o);
-            }
+            for (int db = 0; db < ND; ++db)
+                if (db % REP == rep) orow[16 * db + col] = static_cast<f16>(o[db][e] * inv);
         }
         return;
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int h = 4 * hg + e;
+        if (h >= G) continue;
+        const int64_t prow = (row0 + h) * a.nsplit + split;
+        float* po = a.ws_o + prow * D;
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+            if (db % REP == rep) po[16 * db + col] = o[db][e];
+        if (col == 0 && rep == 0) {
+            a.ws_ml[prow * 2] = m_run[e];
+            a.ws_ml[prow * 2 + 1] = l_tot[e];
+        }
+    }
+}
 
-    // ---- split partial, then the last workgroup of this (b, kv_head) merges.
-    if (lane < LPR) {
+// Log-sum-exp merge of the split partials of one (kv_head, sequence): weights
+// first (lanes over splits, all heads' (m, l) loads in flight at once), then
+// lanes over (head, 8-dim group) accumulate the weighted partials.
+template <int D, int G>
+__global__ void __launch_bounds__(kWave)
+decode_merge_kernel(const DecodeArgs a) {
+    constexpr int LPR = D / 8;
+    constexpr int HPP = kWave / LPR;  // heads per pass
+    __shared__ float w_lds[G][kMaxSplits];
+    __shared__ float l_lds[G][kMaxSplits];
+
+    const int lane = threadIdx.x;
+    const int kvh = blockIdx.x;
+    const int b = blockIdx.y;
+    const int64_t row0 = (int64_t)b * a.Hq + (int64_t)kvh * G;
+    int L = seq_len_of(a, b);
+    if (L > a.cap) L = a.cap;
+    if (L <= 0) return;
+    const int nsb = (L + a.chunk - 1) / a.chunk;
+    if (nsb <= 1) return;  // written directly by the split kernel
+
+    for (int j0 = 0; j0 < nsb; j0 += kWave) {
+        const int j = j0 + lane;
+        float2 v[G];
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float* po = a.ws_o + ((row0 + h) * a.nsplit + split) * D + 8 * lane;
-            *reinterpret_cast<floatx4*>(po) = floatx4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
-            *reinterpret_cast<floatx4*>(po + 4) = floatx4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+        for (int h = 0; h < G; ++h)
+            v[h] = j < nsb ? *reinterpret_cast<const float2*>(a.ws_ml + ((row0 + h) * a.nsplit + j) * 2)
+                           : float2{-INFINITY, 0.f};
+        if (j < nsb) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                w_lds[h][j] = v[h].x;
+                l_lds[h][j] = v[h].y;
+            }
         }
     }
-    if (lane == 0) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float* pm = a.ws_ml + ((row0 + h) * a.nsplit + split) * 2;
-            pm[0] = m_lds[h];
-            pm[1] = lsum[h];
-        }
-    }
-    __threadfence();
-    if (lane == 0) ticket_lds = atomicAdd(a.tickets + (int64_t)b * a.Hkv + kvh, 1u);
     __syncthreads();
-    if (ticket_lds != static_cast<uint32_t>(nsb - 1)) return;
-    __threadfence();
-
-    constexpr int DPL = D / kWave;  // output dims per lane in the merge
+#pragma unroll
     for (int h = 0; h < G; ++h) {
-        const int64_t base = (row0 + h) * a.nsplit;
         float mx = -INFINITY;
-        for (int j = lane; j < nsb; j += kWave) mx = fmaxf(mx, a.ws_ml[(base + j) * 2]);
+        for (int j = lane; j < nsb; j += kWave) mx = fmaxf(mx, w_lds[h][j]);
         mx = wave_max(mx);
         float ls = 0.f;
-        for (int j = lane; j < nsb; j += kWave) {
-            const float w = fast_exp2(a.ws_ml[(base + j) * 2] - mx);
-            w_lds[j] = w;
-            ls += w * a.ws_ml[(base + j) * 2 + 1];
-        }
+        for (int j = lane; j < nsb; j += kWave) ls += l_lds[h][j] * fast_exp2(w_lds[h][j] - mx);
         ls = wave_sum(ls);
-        __syncthreads();
         const float inv = ls > 0.f ? 1.f / ls : 0.f;
-        float o[DPL];
-#pragma unroll
-        for (int u = 0; u < DPL; ++u) o[u] = 0.f;
-        for (int j = 0; j < nsb; ++j) {
-            const float w = w_lds[j];
-            const float* po = a.ws_o + (base + j) * D + DPL * lane;
-#pragma unroll
-            for (int u = 0; u < DPL; ++u) o[u] = fmaf(w, po[u], o[u]);
-        }
-#pragma unroll
-        for (int u = 0; u < DPL; ++u)
-            a.out[(row0 + h) * D + DPL * lane + u] = static_cast<f16>(o[u] * inv);
-        __syncthreads();
+        for (int j = lane; j < nsb; j += kWave) w_lds[h][j] = fast_exp2(w_lds[h][j] - mx) * inv;
     }
-    if (lane == 0) atomicExch(a.tickets + (int64_t)b * a.Hkv + kvh, 0u);
+    __syncthreads();
+#pragma unroll
+    for (int h0 = 0; h0 < G; h0 += HPP) {
+        const int h = h0 + lane / LPR;
+        if (h >= G) continue;
+        const float* po = a.ws_o + (row0 + h) * a.nsplit * D + 8 * (lane % LPR);
+        floatx4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
+        int j = 0;
+        for (; j + 4 <= nsb; j += 4) {
+            floatx4 x[4][2];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                x[u][0] = *reinterpret_cast<const floatx4*>(po + (j + u) * D);
+                x[u][1] = *reinterpret_cast<const floatx4*>(po + (j + u) * D + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float w = w_lds[h][j + u];
+                o0 += w * x[u][0];
+                o1 += w * x[u][1];
+            }
+        }
+        for (; j < nsb; ++j) {
+            const float w = w_lds[h][j];
+            o0 += w * *reinterpret_cast<const floatx4*>(po + j * D);
+            o1 += w * *reinterpret_cast<const floatx4*>(po + j * D + 4);
+        }
+        half8 hv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            hv[e] = static_cast<f16>(o0[e]);
+            hv[4 + e] = static_cast<f16>(o1[e]);
+        }
+        store_half8(a.out + (row0 + h) * D + 8 * (lane % LPR), hv);
+    }
 }
 
 // Any head_dim <= 256, any group size, any page size, any strides: one wave
@@ -452,6 +538,7 @@ decode_generic_kernel(const DecodeArgs a, int D, int G) {
     }
 }
 
+
 // ------------------------------------------------------------- host side --
 struct Plan {
     int nsplit;
@@ -486,11 +573,11 @@ Plan make_plan(int batch, int num_kv_heads, int max_seq_len, int num_splits) {
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 size_t workspace_bytes_for(int batch, int hq, int hkv, int d, const Plan& p) {
+    (void)hkv;
     if (p.nsplit <= 1) return 0;
-    const size_t tickets = align256(sizeof(uint32_t) * (size_t)batch * hkv);
     const size_t o = align256(sizeof(float) * (size_t)batch * hq * p.nsplit * d);
     const size_t ml = align256(sizeof(float) * (size_t)batch * hq * p.nsplit * 2);
-    return tickets + o + ml;
+    return o + ml;
 }
 
 // Library-owned per-device workspace used when the caller passes none.
@@ -540,12 +627,15 @@ bool view_fast_ok(const kvhp_kv_view& v) {
     return v.stride_b % 8 == 0 && v.stride_h % 8 == 0;
 }
 
+
 template <int D, int G>
 void launch_fast(const DecodeArgs& a, dim3 grid, bool paged, hipStream_t s) {
     if (paged)
         hipLaunchKernelGGL((decode_splitk_kernel<D, G, true>), grid, dim3(kWave), 0, s, a);
     else
         hipLaunchKernelGGL((decode_splitk_kernel<D, G, false>), grid, dim3(kWave), 0, s, a);
+    if (a.nsplit > 1)
+        hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.Hkv, grid.z), dim3(kWave), 0, s, a);
 }
 
 template <int D>
@@ -611,13 +701,17 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
     a.Hkv = hkv;
     a.scale_log2 = 1.4426950408889634f / std::sqrt(static_cast<float>(d));
 
+    // The fast kernel reads one block table for K and V (one page id per
+    // token position, the layout PagedKVCache builds).
+    const bool shared_table = !paged || (kv->block_table == vv->block_table &&
+                                         kv->max_pages == vv->max_pages &&
+                                         kv->num_pages == vv->num_pages);
     const bool fast = (d == 64 || d == 128) && fast_group(G) && view_fast_ok(*kv) &&
-                      view_fast_ok(*vv) && aligned16(q) && aligned16(out);
+                      view_fast_ok(*vv) && aligned16(q) && aligned16(out) && shared_table;
     if (!fast) {
         // Single pass: every sequence fully, no workspace.
         a.ws_o = nullptr;
         a.ws_ml = nullptr;
-        a.tickets = nullptr;
         a.chunk = max_seq_len;
         a.nsplit = 1;
         a.cap = max_seq_len;
@@ -641,7 +735,6 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
     const size_t need = workspace_bytes_for(batch, hq, hkv, d, plan);
     a.ws_o = nullptr;
     a.ws_ml = nullptr;
-    a.tickets = nullptr;
     if (need > 0) {
         void* ws = workspace;
         if (!ws) {
@@ -654,11 +747,9 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
             KVHP_REQUIRE(aligned16(ws), KVHP_ERR_INVALID, "decode_attention: workspace not 16-byte aligned");
         }
         char* base = static_cast<char*>(ws);
-        const size_t tk = align256(sizeof(uint32_t) * (size_t)batch * hkv);
         const size_t ob = align256(sizeof(float) * (size_t)batch * hq * plan.nsplit * d);
-        a.tickets = reinterpret_cast<uint32_t*>(base);
-        a.ws_o = reinterpret_cast<float*>(base + tk);
-        a.ws_ml = reinterpret_cast<float*>(base + tk + ob);
+        a.ws_o = reinterpret_cast<float*>(base);
+        a.ws_ml = reinterpret_cast<float*>(base + ob);
     }
     dim3 grid(plan.nsplit, hkv, batch);
     const bool ok = d == 64 ? dispatch_g<64>(G, a, grid, paged, s)

@@ -209,8 +209,8 @@ def test_decode_generic_shapes(hq, hkv, d):
 
 
 def test_decode_caller_workspace_reuse_and_empty_sequences():
-    """A caller workspace is prepared once; consecutive calls (the second
-    smaller) leave its ticket counters clean; zero-length sequences write 0."""
+    """One caller workspace serves consecutive calls (the second smaller, so
+    stale partials from the first are present); zero-length sequences write 0."""
     import torch
     rng = np.random.default_rng(4)
     hq, hkv, d, cap = 32, 8, 128, 3000
@@ -226,5 +226,4 @@ def test_decode_caller_workspace_reuse_and_empty_sequences():
         ref = oracle.decode_attention(q.astype(np.float32), kc.astype(np.float32),
                                       vc.astype(np.float32), np.array(lens, np.int32), hq, hkv, d)
         assert_attn_close(got, ref, f"lens={lens}")
-        ticket_bytes = 256
-        assert int(torch.count_nonzero(ws[:ticket_bytes])) == 0
+        assert np.all(got[np.array(lens) == 0] == 0)
