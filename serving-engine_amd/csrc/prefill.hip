@@ -1,32 +1,35 @@
 // prefill.hip -- causal flash attention for prefill on CDNA4 fp16 MFMA (gfx950).
 //
-// Work decomposition: a 256-thread workgroup (4 waves) owns 64 query rows of
-// one query head; each wave owns 16 rows.  The workgroup walks 64-key tiles
-// from key 0 to the diagonal, staging each K and V tile once in LDS for its
-// four waves.
+// Work decomposition: a 256-thread workgroup (4 waves) owns one KV head and
+// a query block of 16*RB rows for all G query heads of that KV head -- G*RB
+// units of (head, 16 rows), two units per wave (RB = 8/G).  Each 64-key K/V
+// tile is loaded from HBM once, staged in double-buffered LDS, and consumed
+// by every unit, so GQA heads share their K/V traffic.  Query blocks i and
+// N-1-i are processed by the same workgroup, giving every workgroup the same
+// causal work; grid x enumerates (pair, kv_head) with the kv head fastest so
+// a kv head's workgroups land on one XCD (8 KV heads -> x % 8).
 //
-// Per tile and wave, everything is computed transposed so that one lane owns
-// one query row for the whole softmax (no cross-lane row bookkeeping beyond
-// a 4-lane max/sum):
-//   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = K rows from LDS (16 B reads),
-//                 B = Q^T held in registers for the whole loop.
-//                 Lane l gets scores of query row l%16 for keys 4(l/16)+e of
-//                 each 16-key block.
-//   softmax       fp32, log2 domain, causal mask on the diagonal tile only.
-//   O^T += V^T P^T  A = V^T gathered from the LDS V tile, B = P^T converted
-//                 to fp16 in registers straight from the S^T accumulators
-//                 (key slot (g,e) of the k-step maps to key 4g+e of the first
-//                 and 16+4g+e of the second 16-key block, in both operands).
-// Output rows are normalised once at the end and stored as fp16.
+// Per tile and unit, the contraction runs transposed so that one lane owns one
+// query row for the whole online softmax:
+//   S^T = K Q^T     v_mfma_f32_16x16x32_f16, A = K rows (ds_read_b128 from
+//                   LDS, shared by both units), B = Q^T held in registers.
+//                   Lane l gets keys 4(l/16)+e of each 16-key block for query
+//                   row l%16.
+//   softmax         fp32 in the log2 domain; the causal mask is applied only on
+//                   tiles that cross the diagonal; fully masked units skip.
+//   O^T += V^T P^T  A = V^T read with ds_read_b64_tr_b16 (transposing 8-byte
+//                   LDS reads), B = P^T converted to fp16 straight from the S^T
+//                   accumulators: k-slot (g,e') of a 32-key step is key
+//                   4g+e' (e'<4) or 16+4g+e'-4 in both operands.
+// The next tile's global loads are issued before the current tile's MFMAs and
+// written to the other LDS buffer afterwards: one barrier per tile.
 //
-// Scheduling: grid x enumerates query heads so that the G heads of one KV
-// head map to the same XCD (x % 8), y enumerates query blocks longest-first.
-// With a page pool, the workgroups of the first query head of each KV group
-// also write the K/V rows of their own 64-key diagonal tile into the pages
-// (every key row is written exactly once, from registers already loaded).
+// With a page pool, each workgroup also writes the K/V rows of its own query
+// block into the pages from the registers it already loaded (every key row is
+// written exactly once, bit-exact).
 //
 // Roofline: MFMA-bound for long prompts; algorithmic work 4*D*Hq*S(S+1)/2
-// flops (two causal contractions).
+// flops (the two causal contractions).
 #include "kvhp_internal.h"
 
 #include <cmath>
@@ -35,9 +38,7 @@ namespace kvhp {
 
 namespace {
 
-constexpr int kBM = 64;     // query rows per workgroup
 constexpr int kBN = 64;     // keys per tile
-constexpr int kThreads = 256;
 
 struct PrefillArgs {
     const f16* q;           // [B][S][Hq][D]
@@ -50,171 +51,312 @@ struct PrefillArgs {
     int max_pages;
     int num_pages;
     int S, Hq, Hkv, G;
+    int RB;                 // 16-row blocks per query block (fast kernel)
     int n_qblk;
     float scale_log2;
 };
 
-template <int D>
-__global__ void __launch_bounds__(kThreads)
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+typedef __attribute__((address_space(3))) f16 lds_f16;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// ds_read_b64_tr_b16: within each 16-lane block, lane i receives element
+// (i % 4) of the 8-byte groups addressed by lanes 4k + i/4, k = 0..3.
+__device__ __forceinline__ short4v lds_read_tr16(const f16* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(lds_f16*)p);
+}
+
+__device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
+    return __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// global_load_lds_dwordx4: lane l's 16 bytes land at lds_base + 16*l (M0
+// holds the wave-uniform LDS base).  Issued as inline asm so that only the
+// explicit vmcnt waits of the ring order it against the LDS reads: the
+// compiler's own tracking cannot tell ring stages apart and would otherwise
+// drain every in-flight stage before each read.
+__device__ __forceinline__ void dma16(const f16* src, f16* lds_base) {
+    const uint32_t m0v = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((lds_void*)(lds_f16*)lds_base));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :: "s"(m0v), "v"(src) : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) (expcnt / lgkmcnt left free).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Orders this wave's LDS accesses across the barrier without the vmcnt(0)
+// drain a __syncthreads() fence implies (which would empty the DMA ring).
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// A workgroup serves one KV head and a query block of 16*RB rows for all G
+// query heads of that KV head: G*RB "units" of (head, 16 rows), at most 8,
+// two per wave.  K/V tiles of 64 keys stream through a 4-stage LDS ring
+// filled by direct global->LDS loads; rows are stored XOR-swizzled (16-byte
+// chunk c of row r at position c ^ swz(r)) so the MFMA operand reads hit
+// distinct banks without padding.  Query blocks i and N-1-i run in the same
+// workgroup so every workgroup does the same causal work.
+template <int D, int WAVES>
+__global__ void __launch_bounds__(WAVES * kWave)
 prefill_mfma_kernel(const PrefillArgs a) {
+    constexpr int NTH = WAVES * kWave;  // threads per workgroup
+    constexpr int NB = 8 / WAVES;       // units per wave (8 units per workgroup)
     constexpr int NC = D / 32;          // k-chunks of the QK contraction
     constexpr int ND = D / 16;          // 16-dim blocks of the output
     constexpr int CPR = D / 8;          // 16-byte chunks per row
-    constexpr int LDR = D + 8;          // LDS row pitch in halfs (bank skew)
-    constexpr int LOADS = kBN * CPR / kThreads;
+    constexpr int RPI = kWave / CPR;    // rows per DMA instruction
+    constexpr int IPW = kBN / RPI / WAVES;  // DMA instructions per wave per matrix
+    constexpr int LPT = 2 * IPW;        // DMA loads per wave per tile (K + V)
+    constexpr int TB = kBN * D;         // halfs per tile matrix
+    constexpr int KSW = CPR - 1;        // K swizzle: c ^ (r & KSW)
+    constexpr int VSW = CPR / 2 - 1;    // V swizzle: c ^ ((r & VSW) << 1)
 
-    __shared__ f16 Ks[kBN * LDR];
-    __shared__ f16 Vs[kBN * LDR];
+    __shared__ __attribute__((aligned(16))) f16 st0[2 * TB];
+    __shared__ __attribute__((aligned(16))) f16 st1[2 * TB];
+    __shared__ __attribute__((aligned(16))) f16 st2[2 * TB];
+    __shared__ __attribute__((aligned(16))) f16 st3[2 * TB];
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases in SGPRs
     const int lane = tid & 63;
     const int g = lane >> 4;
     const int col = lane & 15;
 
     const int kvh = blockIdx.x % a.Hkv;
-    const int qh = kvh * a.G + blockIdx.x / a.Hkv;
-    const int qblk = a.n_qblk - 1 - (int)blockIdx.y;
-    const int b = blockIdx.z;
-    const int q0 = qblk * kBM;
+    const int pair = blockIdx.x / a.Hkv;
+    const int b = blockIdx.y;
     const int S = a.S;
-    const int64_t qrow_stride = (int64_t)a.Hq * D;
-    const int64_t kvrow_stride = (int64_t)a.Hkv * D;
-    const f16* qb = a.q + (int64_t)b * S * qrow_stride + (int64_t)qh * D;
-    const f16* kb = a.k + (int64_t)b * S * kvrow_stride + (int64_t)kvh * D;
-    const f16* vb = a.v + (int64_t)b * S * kvrow_stride + (int64_t)kvh * D;
-    const bool write_pages = a.pool_k != nullptr && (qh % a.G) == 0;
+    const int G = a.G;
+    const int RB = a.RB;
+    const int BM = 16 * RB;
+    const int nunits = G * RB;
+    const int64_t qrs = (int64_t)a.Hq * D;     // q/out row stride
+    const int64_t kvrs = (int64_t)a.Hkv * D;   // k/v row stride
+    const f16* kb = a.k + (int64_t)b * S * kvrs + (int64_t)kvh * D;
+    const f16* vb = a.v + (int64_t)b * S * kvrs + (int64_t)kvh * D;
 
-    // This lane's query row, as the B operand (Q^T): dims 32c + 8g .. +8.
-    const int my_row = q0 + wave * 16 + col;
-    half8 qop[NC];
-    if (my_row < S) {
+    // DMA of tile tt into a stage: this wave's rows (wave*IPW + p)*RPI + lane/CPR.
+    // Tiles past the last one re-load the last tile (an L2 hit): every path
+    // issues the same loads, so the vmcnt bookkeeping stays exact.
+    int last_tile = 0;
+    auto issue = [&](f16* stg, int tt) {
+        tt = min(tt, last_tile);
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
-            qop[c] = load_half8(qb + (int64_t)my_row * qrow_stride + 32 * c + 8 * g);
-    } else {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) qop[c] = half8{};
-    }
+        for (int p = 0; p < IPW; ++p) {
+            const int blk = wave * IPW + p;
+            const int row = blk * RPI + lane / CPR;
+            const int key = min(tt * kBN + row, S - 1);
+            const int ck = (lane % CPR) ^ (row & KSW);
+            const int cv = (lane % CPR) ^ ((row & VSW) << 1);
+            dma16(kb + (int64_t)key * kvrs + 8 * ck, stg + blk * RPI * D);
+            dma16(vb + (int64_t)key * kvrs + 8 * cv, stg + TB + blk * RPI * D);
+        }
+    };
 
-    floatx4 o[ND];
-#pragma unroll
-    for (int i = 0; i < ND; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -1e30f;
-    float l_part = 0.f;
+    for (int pass = 0; pass < 2; ++pass) {
+        const int qblk = pass == 0 ? pair : a.n_qblk - 1 - pair;
+        if (pass == 1 && qblk <= pair) break;   // odd count: middle block once
+        const int q0 = qblk * BM;
 
-    const int last_row = min(q0 + kBM, S) - 1;
-    const int n_tiles = last_row / kBN + 1;
-    const int wave_last_row = q0 + wave * 16 + 15;
-
-    for (int kt = 0; kt < n_tiles; ++kt) {
-        const int k0 = kt * kBN;
-        __syncthreads();
-        // ---- stage K and V tiles (rows past S are zero).
+        // ---- this wave's units: u = wave + WAVES*i -> head kvh*G + u%G, rows r0..r0+15
+        int r0[NB], qh[NB];
+        bool uvalid[NB];
+        half8 qop[NB][NC];
 #pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int idx = i * kThreads + tid;
-            const int r = idx / CPR;
-            const int ch = idx % CPR;
-            const int key = k0 + r;
-            half8 kv = {}, vv = {};
-            if (key < S) {
-                kv = load_half8(kb + (int64_t)key * kvrow_stride + 8 * ch);
-                vv = load_half8(vb + (int64_t)key * kvrow_stride + 8 * ch);
-                if (write_pages && key >= q0 && key / kPage < a.max_pages) {
-                    int pid = a.bt[(int64_t)b * a.max_pages + key / kPage];
-                    if (pid >= 0 && pid < a.num_pages) {
-                        const int64_t dst =
-                            (((int64_t)kvh * a.num_pages + pid) * kPage + key % kPage) * D + 8 * ch;
-                        store_half8(a.pool_k + dst, kv);
-                        store_half8(a.pool_v + dst, vv);
+        for (int i = 0; i < NB; ++i) {
+            const int u = wave + WAVES * i;
+            uvalid[i] = u < nunits;
+            qh[i] = kvh * G + (uvalid[i] ? u % G : 0);
+            r0[i] = q0 + 16 * (uvalid[i] ? u / G : 0);
+            const int row = r0[i] + col;
+            const bool live = uvalid[i] && row < S;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+                qop[i][c] = live ? load_half8(a.q + ((int64_t)b * S + row) * qrs +
+                                              (int64_t)qh[i] * D + 32 * c + 8 * g)
+                                 : half8{};
+        }
+        floatx4 o[NB][ND];
+        float m_run[NB], l_part[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            m_run[i] = -1e30f;
+            l_part[i] = 0.f;
+#pragma unroll
+            for (int db = 0; db < ND; ++db) o[i][db] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+
+        const int last_row = min(q0 + BM, S) - 1;
+        const int n_tiles = last_row / kBN + 1;
+        last_tile = n_tiles - 1;
+
+        wait_vmcnt<0>();  // q in registers before the ring: no compiler waits inside it
+        ring_barrier();   // everyone is done with the previous pass's stages
+        issue(st0, 0);
+        issue(st1, 1);
+        issue(st2, 2);
+
+        // One tile on stage STG: wait for this wave's DMA of the tile (the two
+        // later tiles stay in flight), barrier (all waves' DMA landed, the
+        // previous stage is free), refill the previous stage with tile kt+3,
+        // compute.
+        auto step = [&](f16* stg, f16* next_stg, int kt) {
+            wait_vmcnt<2 * LPT>();
+            ring_barrier();
+            issue(next_stg, kt + 3);
+
+            const int k0 = kt * kBN;
+            const f16* Kt = stg;
+            const f16* Vt = stg + TB;
+
+            // ---- S^T = K Q^T for both units, K operand shared.
+            bool act[NB];
+#pragma unroll
+            for (int i = 0; i < NB; ++i) act[i] = uvalid[i] && k0 <= r0[i] + 15;
+            floatx4 sc[NB][4];
+#pragma unroll
+            for (int i = 0; i < NB; ++i)
+#pragma unroll
+                for (int kb4 = 0; kb4 < 4; ++kb4) sc[i][kb4] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb4 = 0; kb4 < 4; ++kb4) {
+                const int r = 16 * kb4 + col;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const int pos = (4 * c + g) ^ (r & KSW);
+                    const half8 kop = *reinterpret_cast<const half8*>(&Kt[r * D + 8 * pos]);
+#pragma unroll
+                    for (int i = 0; i < NB; ++i)
+                        sc[i][kb4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[i][c],
+                                                                            sc[i][kb4], 0, 0, 0);
+                }
+            }
+
+            // ---- online softmax per unit; P^T operands straight from S^T.
+            // Inactive units (invalid, or entirely above the diagonal) see
+            // only -inf scores: alpha = 1 and p = 0 leave their state as is,
+            // so every MFMA above and below runs unconditionally (no
+            // branches, no conservative waits inside the ring).  The running
+            // max is kept on raw scores (scale > 0), and the scale is folded
+            // into the exp2 argument: p = 2^(s*c - m*c).
+            half8 pop[NB][2];
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int row = r0[i] + col;
+                const bool diag = !act[i] || k0 + kBN - 1 > r0[i];
+                if (diag) {
+#pragma unroll
+                    for (int kb4 = 0; kb4 < 4; ++kb4) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int key = k0 + 16 * kb4 + 4 * g + e;
+                            if (!act[i] || key > row || key >= S) sc[i][kb4][e] = -INFINITY;
+                        }
                     }
                 }
+                float tmax = -INFINITY;
+#pragma unroll
+                for (int kb4 = 0; kb4 < 4; ++kb4)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, sc[i][kb4][e]);
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+                const float mn = fmaxf(m_run[i], tmax);
+                const float nmc = -mn * a.scale_log2;
+                float ls = 0.f;
+#pragma unroll
+                for (int kb4 = 0; kb4 < 4; ++kb4) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float p = fast_exp2(fmaf(sc[i][kb4][e], a.scale_log2, nmc));
+                        pop[i][kb4 / 2][(kb4 % 2) * 4 + e] = static_cast<f16>(p);
+                        ls += p;
+                    }
+                }
+                // Rescale only when some row's max moved (rare after the first
+                // tiles): a wave-uniform branch.
+                if (__builtin_amdgcn_read_exec() & __ballot(mn != m_run[i])) {
+                    const float alpha = fast_exp2((m_run[i] - mn) * a.scale_log2);
+                    l_part[i] *= alpha;
+#pragma unroll
+                    for (int db = 0; db < ND; ++db) o[i][db] *= alpha;
+                }
+                m_run[i] = mn;
+                l_part[i] += ls;
             }
-            *reinterpret_cast<half8*>(&Ks[r * LDR + 8 * ch]) = kv;
-            *reinterpret_cast<half8*>(&Vs[r * LDR + 8 * ch]) = vv;
-        }
-        __syncthreads();
-        if (k0 > wave_last_row) continue;  // tile entirely above this wave's rows
 
-        // ---- S^T = K Q^T: four 16-key blocks.
-        floatx4 sc[4];
+            // ---- O^T += V^T P^T; k-slot (g,e') of step ks is key
+            //      ks*32 + (e' < 4 ? 4g + e' : 16 + 4g + e' - 4).
 #pragma unroll
-        for (int kb4 = 0; kb4 < 4; ++kb4) {
-            sc[kb4] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int ks = 0; ks < 2; ++ks) {
+                const int R1 = 32 * ks + 4 * g + col / 4;
+                const int R2 = R1 + 16;
+                const int h = 4 * ((col % 4) & 1);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const half8 kop =
-                    *reinterpret_cast<const half8*>(&Ks[(16 * kb4 + col) * LDR + 32 * c + 8 * g]);
-                sc[kb4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[c], sc[kb4], 0, 0, 0);
+                for (int db = 0; db < ND; ++db) {
+                    const int c = 2 * db + ((col % 4) >> 1);
+                    const f16* p1 = &Vt[R1 * D + 8 * (c ^ ((R1 & VSW) << 1)) + h];
+                    const f16* p2 = &Vt[R2 * D + 8 * (c ^ ((R2 & VSW) << 1)) + h];
+                    const half8 vop = cat_half8(lds_read_tr16(p1), lds_read_tr16(p2));
+#pragma unroll
+                    for (int i = 0; i < NB; ++i)
+                        o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[i][ks],
+                                                                          o[i][db], 0, 0, 0);
+                }
             }
-        }
-        // ---- mask, running max for this lane's row (shared by 4 lanes).
-        const bool diag = k0 + kBN - 1 > q0 + wave * 16;
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int kb4 = 0; kb4 < 4; ++kb4) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int key = k0 + 16 * kb4 + 4 * g + e;
-                float x = sc[kb4][e] * a.scale_log2;
-                if (diag && (key > my_row || key >= S)) x = -INFINITY;
-                sc[kb4][e] = x;
-                tmax = fmaxf(tmax, x);
-            }
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float mn = fmaxf(m_run, tmax);
-        const float alpha = fast_exp2(m_run - mn);
-        m_run = mn;
-        l_part *= alpha;
-#pragma unroll
-        for (int i = 0; i < ND; ++i) o[i] *= alpha;
+        };
 
-        // ---- P^T operands (fp16) for the two 32-key k-steps.
-        half8 pop[2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float p0 = fast_exp2(sc[2 * ks][e] - mn);
-                const float p1 = fast_exp2(sc[2 * ks + 1][e] - mn);
-                l_part += p0 + p1;
-                pop[ks][e] = static_cast<f16>(p0);
-                pop[ks][4 + e] = static_cast<f16>(p1);
-            }
+        for (int kt = 0; kt < n_tiles; kt += 4) {
+            step(st0, st3, kt);
+            if (kt + 1 < n_tiles) step(st1, st0, kt + 1);
+            if (kt + 2 < n_tiles) step(st2, st1, kt + 2);
+            if (kt + 3 < n_tiles) step(st3, st2, kt + 3);
         }
-        // ---- O^T += V^T P^T.
+        wait_vmcnt<0>();  // drain the ring's trailing re-loads
+
+        // ---- normalise and store: lane holds row r0+col, dims 16db + 4g + e.
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int i = 0; i < NB; ++i) {
+            float lt = l_part[i];
+            lt += __shfl_xor(lt, 16);
+            lt += __shfl_xor(lt, 32);
+            const int row = r0[i] + col;
+            if (!uvalid[i] || row >= S) continue;
+            const float inv = lt > 0.f ? 1.f / lt : 0.f;
+            f16* orow = a.out + ((int64_t)b * S + row) * qrs + (int64_t)qh[i] * D;
 #pragma unroll
             for (int db = 0; db < ND; ++db) {
-                half8 vop;
-                const int d = 16 * db + col;
+                half4 hv;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    vop[e] = Vs[(32 * ks + 4 * g + e) * LDR + d];
-                    vop[4 + e] = Vs[(32 * ks + 16 + 4 * g + e) * LDR + d];
-                }
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[ks], o[db], 0, 0, 0);
+                for (int e = 0; e < 4; ++e) hv[e] = static_cast<f16>(o[i][db][e] * inv);
+                *reinterpret_cast<half4*>(orow + 16 * db + 4 * g) = hv;
             }
         }
-    }
 
-    float l_tot = l_part;
-    l_tot += __shfl_xor(l_tot, 16);
-    l_tot += __shfl_xor(l_tot, 32);
-    if (my_row < S) {
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        f16* orow = a.out + ((int64_t)b * S + my_row) * qrow_stride + (int64_t)qh * D;
-#pragma unroll
-        for (int db = 0; db < ND; ++db) {
-            half4 h;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = static_cast<f16>(o[db][e] * inv);
-            *reinterpret_cast<half4*>(orow + 16 * db + 4 * g) = h;
+        // ---- pages: this query block's own K/V rows, once per KV head.
+        if (a.pool_k) {
+            for (int idx = tid; idx < BM * CPR; idx += NTH) {
+                const int key = q0 + idx / CPR;
+                const int ch = idx % CPR;
+                if (key >= S || key / kPage >= a.max_pages) continue;
+                const int pid = a.bt[(int64_t)b * a.max_pages + key / kPage];
+                if (pid < 0 || pid >= a.num_pages) continue;
+                const int64_t dst =
+                    (((int64_t)kvh * a.num_pages + pid) * kPage + key % kPage) * D + 8 * ch;
+                store_half8(a.pool_k + dst, load_half8(kb + (int64_t)key * kvrs + 8 * ch));
+                store_half8(a.pool_v + dst, load_half8(vb + (int64_t)key * kvrs + 8 * ch));
+            }
         }
+        wait_vmcnt<0>();   // page stores complete before the next ring starts
     }
 }
 
@@ -317,16 +459,23 @@ int prefill_impl(const void* q, const void* k, const void* v, void* out, int64_t
     a.Hkv = hkv;
     a.G = hq / hkv;
     a.scale_log2 = 1.4426950408889634f / std::sqrt(static_cast<float>(d));
-    a.n_qblk = static_cast<int>((seq_len + kBM - 1) / kBM);
+    a.RB = 1;
+    a.n_qblk = 0;
 
-    const bool fast = (d == 64 || d == 128) && aligned16(q) && aligned16(k) && aligned16(v) &&
-                      aligned16(out) && (!pool_k || (aligned16(pool_k) && aligned16(pool_v)));
+    const bool fast = (d == 64 || d == 128) && a.G <= 8 && aligned16(q) && aligned16(k) &&
+                      aligned16(v) && aligned16(out) &&
+                      (!pool_k || (aligned16(pool_k) && aligned16(pool_v)));
     if (fast) {
-        dim3 grid(hq, a.n_qblk, batch);
+        // units of (head, 16 rows) per workgroup: G*RB <= 8, two per wave
+        a.RB = 8 / a.G;
+        const int bm = 16 * a.RB;
+        a.n_qblk = static_cast<int>((seq_len + bm - 1) / bm);
+        dim3 grid(hkv * ((a.n_qblk + 1) / 2), batch);
+        constexpr int W = 8;  // waves per workgroup: one 16-row unit each
         if (d == 64)
-            hipLaunchKernelGGL(prefill_mfma_kernel<64>, grid, dim3(kThreads), 0, s, a);
+            hipLaunchKernelGGL((prefill_mfma_kernel<64, W>), grid, dim3(W * kWave), 0, s, a);
         else
-            hipLaunchKernelGGL(prefill_mfma_kernel<128>, grid, dim3(kThreads), 0, s, a);
+            hipLaunchKernelGGL((prefill_mfma_kernel<128, W>), grid, dim3(W * kWave), 0, s, a);
         return check_launch("flash_prefill");
     }
     dim3 grid(hq, static_cast<unsigned>(seq_len), batch);
