@@ -50,9 +50,11 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 2 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4")
-    ap.add_argument("--profile", action="store_true",
+    ap.add_argument("--profile", nargs="?", const="decode", default=None,
+                    choices=("decode", "prefill"),
                     help="short run for rocprofv3: a 256 MiB device copy (counter "
-                         "calibration) then the config-3 steps; no CPU baseline, no extras")
+                         "calibration) then the config-3 steps (decode) or config-4 "
+                         "S=2048 prefill calls (prefill); no CPU baseline, no extras")
     return ap.parse_args()
 
 
@@ -276,11 +278,11 @@ def run_config2(torch, kvhp):
     return {"workload": "config2: B=1, 32/8 heads, D=128, contiguous fp16 KV, flushed", "rows": rows}
 
 
-def run_config4(torch, kvhp):
+def run_config4(torch, kvhp, sizes=(512, 2048, 8192), reps=10):
     hq, hkv, d = 32, 8, 128
     rows = []
     fl = Flusher(torch)
-    for s in (512, 2048, 8192):
+    for s in sizes:
         g = torch.Generator(device="cuda").manual_seed(s)
         q = torch.randn((s, hq, d), generator=g, device="cuda").half()
         k = torch.randn((s, hkv, d), generator=g, device="cuda").half()
@@ -292,7 +294,7 @@ def run_config4(torch, kvhp):
 
         for _ in range(3):
             fn()
-        med, _ = time_op(torch, fn, 10, fl)
+        med, _ = time_op(torch, fn, reps, fl)
         flops = 2.0 * d * hq * s * (s + 1)
         tf = flops / med / 1e6
         rows.append({"S": s, "us": round(med, 2), "TFLOP/s": round(tf, 1),
@@ -336,6 +338,10 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+        if args.profile == "prefill":
+            r4 = run_config4(torch, kvhp, sizes=(2048,), reps=args.steps)
+            print(json.dumps({"profile": "prefill", "config4": r4}))
+            return
     log("config3 timed steps ...")
     r = run_config3(torch, kvhp, args)
     c = r.pop("c")

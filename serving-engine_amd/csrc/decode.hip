@@ -551,10 +551,18 @@ Plan make_plan(int batch, int num_kv_heads, int max_seq_len, int num_splits) {
     const int max_by_chunk = (max_seq_len + 63) / 64;  // chunks of >= 64 tokens
     int s = num_splits;
     if (s <= 0) {
-        // Aim for ~16 resident waves per CU over 256 CUs, no chunk below 64.
+        // Measured on MI355X (B=1..32, L=512..64K, D=64/128): chunks of about
+        // L/64 tokens but never below 128, and at most ~6144 workgroups in
+        // the grid.  Longer chunks starve the long sequences of a ragged
+        // batch; shorter ones make the merge and per-workgroup set-up cost
+        // more than they hide.
         const int64_t units = (int64_t)batch * num_kv_heads;
-        const int64_t target = 4096;
-        s = static_cast<int>((target + units - 1) / units);
+        int per_split = (max_seq_len + 63) / 64;
+        if (per_split < 128) per_split = 128;
+        per_split = (per_split + 63) / 64 * 64;
+        s = (max_seq_len + per_split - 1) / per_split;
+        const int64_t grid_cap = units >= 6144 ? 1 : 6144 / units;
+        if (s > grid_cap) s = static_cast<int>(grid_cap);
     }
     if (s > max_by_chunk) s = max_by_chunk;
     if (s < 1) s = 1;
@@ -570,14 +578,14 @@ Plan make_plan(int batch, int num_kv_heads, int max_seq_len, int num_splits) {
     return p;
 }
 
-size_t align256(size_t x) { return (x + 255) / 256 * 256; }
-
+// Workspace = fp32 o[B*Hq][nsplit][D] followed by (m, l)[B*Hq][nsplit]:
+// exactly nsplit*B*Hq*(D+2) floats, the split_buffer size the reference's
+// callers allocate (forward_gpu.cu:100, test_attention.cpp:124).  Only the
+// fast kernels (D = 64 or 128) split, so the (m, l) block stays 16-B aligned.
 size_t workspace_bytes_for(int batch, int hq, int hkv, int d, const Plan& p) {
     (void)hkv;
     if (p.nsplit <= 1) return 0;
-    const size_t o = align256(sizeof(float) * (size_t)batch * hq * p.nsplit * d);
-    const size_t ml = align256(sizeof(float) * (size_t)batch * hq * p.nsplit * 2);
-    return o + ml;
+    return sizeof(float) * (size_t)batch * hq * p.nsplit * (d + 2);
 }
 
 // Library-owned per-device workspace used when the caller passes none.
@@ -747,7 +755,7 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
             KVHP_REQUIRE(aligned16(ws), KVHP_ERR_INVALID, "decode_attention: workspace not 16-byte aligned");
         }
         char* base = static_cast<char*>(ws);
-        const size_t ob = align256(sizeof(float) * (size_t)batch * hq * plan.nsplit * d);
+        const size_t ob = sizeof(float) * (size_t)batch * hq * plan.nsplit * d;
         a.ws_o = reinterpret_cast<float*>(base);
         a.ws_ml = reinterpret_cast<float*>(base + ob);
     }

@@ -1,0 +1,534 @@
+// test_engine.cpp -- tests of the C++ API (serving-engine_amd/engine/*.h)
+// written the way the reference's own C++ tests exercise engine::cuda and
+// engine::KVCache (reference tests/test_kv_cache.cpp:43-200,
+// tests/test_attention.cpp:34-291): random shapes, fp16-rounded inputs,
+// GPU result against a CPU reference.  Here the CPU reference is the oracle
+// (oracle/kvhp_oracle.h), and the tolerance is |g - r| <= 2e-3 + 1e-2 |r|
+// per element plus max |g - r| <= 2e-3, stricter than the reference's 3e-3
+// / 3.5e-3 max-abs.  Copies are checked bit for bit.
+//
+//   test_engine --cpu   cases that need no GPU (fp16 conversion, host
+//                       validation errors, page bookkeeping)
+//   test_engine --gpu   every case
+// Exit status 0 when every check passed.
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "hip_utils.h"
+#include "half.h"
+#include "kernels.h"
+#include "kv_cache.h"
+#include "kv_view.h"
+#include "kvhp_oracle.h"
+
+using namespace engine;
+
+namespace {
+
+int g_checks = 0;
+int g_failures = 0;
+std::string g_case;
+
+#define EXPECT(cond, ...)                                                          \
+    do {                                                                           \
+        ++g_checks;                                                                \
+        if (!(cond)) {                                                             \
+            ++g_failures;                                                          \
+            if (g_failures < 40) {                                                 \
+                std::printf("  FAIL [%s] %s:%d: %s -- ", g_case.c_str(), __FILE__, \
+                            __LINE__, #cond);                                      \
+                std::printf(__VA_ARGS__);                                          \
+                std::printf("\n");                                                 \
+            }                                                                      \
+        }                                                                          \
+    } while (0)
+
+std::vector<half> random_half(std::mt19937& rng, size_t n, float lo, float hi) {
+    std::uniform_real_distribution<float> dist(lo, hi);
+    std::vector<half> v(n);
+    for (auto& x : v) x = float_to_half(dist(rng));
+    return v;
+}
+
+std::vector<float> to_float(const std::vector<half>& h) {
+    std::vector<float> f(h.size());
+    for (size_t i = 0; i < h.size(); ++i) f[i] = half_to_float(h[i]);
+    return f;
+}
+
+template <typename T>
+DeviceBuffer<T> upload(const std::vector<T>& v) {
+    DeviceBuffer<T> d(v.size());
+    d.copy_from_host(v.data(), v.size());
+    return d;
+}
+
+template <typename T>
+std::vector<T> download(const DeviceBuffer<T>& d) {
+    std::vector<T> v(d.size());
+    d.copy_to_host(v.data(), v.size());
+    return v;
+}
+
+// Compares fp16 GPU output with an fp32 reference; returns the max abs diff.
+float check_close(const std::vector<half>& got, const std::vector<float>& ref, const char* what) {
+    float worst = 0.f;
+    size_t bad = 0, first_bad = 0;
+    for (size_t i = 0; i < ref.size(); ++i) {
+        const float g = half_to_float(got[i]);
+        const float d = std::fabs(g - ref[i]);
+        if (!(d <= 2e-3f + 1e-2f * std::fabs(ref[i]))) {
+            if (!bad) first_bad = i;
+            ++bad;
+        }
+        if (!(d <= worst)) worst = d;
+    }
+    EXPECT(bad == 0 && worst <= 2e-3f, "%s: %zu elements out of tolerance (first %zu), max abs %.3g",
+           what, bad, first_bad, worst);
+    return worst;
+}
+
+bool bits_equal(const std::vector<half>& a, const std::vector<half>& b) {
+    return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * sizeof(half)) == 0;
+}
+
+// ------------------------------------------------------------- CPU cases --
+
+void case_half_conversion() {
+    // every binary16 pattern survives half -> float -> half (NaNs stay NaN)
+    // and agrees with the oracle's independent conversion
+    for (uint32_t b = 0; b < 65536; ++b) {
+        const half h{(uint16_t)b};
+        const float f = half_to_float(h);
+        const float fo = kvo_f16_to_f32((uint16_t)b);
+        const bool nan = ((b >> 10) & 0x1f) == 0x1f && (b & 0x3ff);
+        if (nan) {
+            EXPECT(std::isnan(f), "pattern %04x", b);
+            continue;
+        }
+        EXPECT(std::memcmp(&f, &fo, 4) == 0, "pattern %04x -> %g vs oracle %g", b, f, fo);
+        EXPECT(float_to_half(f).bits == b, "pattern %04x round trip", b);
+    }
+    // float -> half rounding (ties to even, subnormals, overflow) against the
+    // oracle over random bit patterns and the halfway points of every
+    // adjacent pair of finite halves
+    std::mt19937 rng(11);
+    for (int i = 0; i < 2000000; ++i) {
+        uint32_t x = rng();
+        float f;
+        std::memcpy(&f, &x, 4);
+        if (std::isnan(f)) continue;
+        EXPECT(float_to_half(f).bits == kvo_f32_to_f16(f), "float bits %08x", x);
+    }
+    for (uint32_t b = 0; b < 0x7bff; ++b) {
+        const double lo = half_to_float(half{(uint16_t)b});
+        const double hi = half_to_float(half{(uint16_t)(b + 1)});
+        const float mid = (float)((lo + hi) / 2);  // exact in float
+        EXPECT(float_to_half(mid).bits == kvo_f32_to_f16(mid), "tie above %04x", b);
+        EXPECT(float_to_half(-mid).bits == kvo_f32_to_f16(-mid), "tie below -%04x", b);
+    }
+}
+
+void case_host_validation() {
+    // Hq not a multiple of Hkv, and head_dim beyond 256, are rejected before
+    // any device work, as a thrown std::runtime_error
+    half dummy[8] = {};
+    hip::KVView v{dummy, 0, 0, 8, 1};
+    int lens = 1;
+    bool threw = false;
+    try {
+        hip::decode_gqa_split(dummy, v, v, &lens, dummy, 1, 6, 4, 64, 16);
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find("num_q_heads") != std::string::npos;
+    }
+    EXPECT(threw, "decode_gqa_split accepted Hq=6, Hkv=4");
+    threw = false;
+    try {
+        hip::flash_prefill_gqa(dummy, dummy, dummy, dummy, 4, 4, 4, 512, 1);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    EXPECT(threw, "flash_prefill_gqa accepted head_dim=512");
+    // empty work is a no-op, as in the reference (kv_cache.cu:50)
+    bool ok = true;
+    try {
+        hip::append_kv_cache(dummy, dummy, dummy, dummy, 0, 0, 1, 16, 8);
+        hip::decode_gqa(dummy, dummy, dummy, dummy, 0, 4, 4, 16, 8);
+    } catch (...) {
+        ok = false;
+    }
+    EXPECT(ok, "empty work threw");
+    // the reference-signature split buffer holds 8 splits' worth of partials
+    EXPECT(hip::decode_split_buffer_floats(3, 14, 64) == (size_t)8 * 3 * 14 * 66, "size");
+    EXPECT(hip::decode_workspace_bytes(3, 14, 2, 64, 600, 8) <=
+               hip::decode_split_buffer_floats(3, 14, 64) * sizeof(float),
+           "8-split workspace larger than the split buffer");
+}
+
+// ------------------------------------------------------------- GPU cases --
+
+void case_kv_cache_layout() {
+    // pointer arithmetic of reference kv_cache.h:34-53
+    KVCache c(3, 4, 64, 40);
+    const size_t per = (size_t)4 * 40 * 64;
+    EXPECT(c.get_layer_ptr(0, 0) == c.raw_data(), "layer 0 K");
+    EXPECT(c.get_layer_ptr(1, 1) == c.raw_data() + 3 * per, "layer 1 V");
+    EXPECT(c.get_head_ptr(2, 1, 3) == c.raw_data() + 5 * per + 3 * 40 * 64, "head ptr");
+    EXPECT(c.current_seq_len() == 0, "fresh length");
+    c.set_current_seq_len(7);
+    EXPECT(c.current_seq_len() == 7, "length");
+    // allocate() zeroes the cache
+    std::vector<half> all((size_t)3 * 2 * per);
+    HIP_CHECK(hipMemcpy(all.data(), c.raw_data(), all.size() * 2, hipMemcpyDeviceToHost));
+    bool zero = true;
+    for (auto h : all) zero &= h.bits == 0;
+    EXPECT(zero, "cache not zeroed");
+}
+
+void case_append_kv_cache() {
+    // 25 random shapes (reference test_kv_cache.cpp:43-97), bit-exact
+    std::mt19937 rng(1101);
+    for (int it = 0; it < 25; ++it) {
+        const int T = it == 0 ? 1 : 1 + (int)(rng() % 37);
+        const int start = it == 0 ? 0 : (int)(rng() % 50);
+        const int hkv = 1 + (int)(rng() % 4);
+        // some shapes run past max_seq: those positions must be dropped
+        const int max_seq = start + T + (int)(rng() % 30) - (it % 5 == 4 ? T / 2 : 0);
+        const int d = 16 * (1 + (int)(rng() % 8));
+        auto ks = random_half(rng, (size_t)T * hkv * d, -2, 2);
+        auto vs = random_half(rng, (size_t)T * hkv * d, -2, 2);
+        const size_t csz = (size_t)hkv * max_seq * d;
+        auto dk = upload(ks), dv = upload(vs);
+        DeviceBuffer<half> ck(csz), cv(csz);
+        ck.zero();
+        cv.zero();
+        hip::append_kv_cache(dk.data(), dv.data(), ck.data(), cv.data(), T, start, hkv, max_seq, d);
+        HIP_CHECK(hipDeviceSynchronize());
+        std::vector<uint16_t> rk(csz, 0), rv(csz, 0);
+        kvo_append_kv(reinterpret_cast<const uint16_t*>(ks.data()),
+                      reinterpret_cast<const uint16_t*>(vs.data()), rk.data(), rv.data(), T, start,
+                      hkv, max_seq, d);
+        auto gk = download(ck), gv = download(cv);
+        EXPECT(std::memcmp(gk.data(), rk.data(), csz * 2) == 0, "K shape %d (T=%d start=%d hkv=%d max_seq=%d d=%d)", it, T, start, hkv, max_seq, d);
+        EXPECT(std::memcmp(gv.data(), rv.data(), csz * 2) == 0, "V shape %d", it);
+    }
+}
+
+void case_decode_gqa() {
+    // 25 random shapes over a head-major cache (test_kv_cache.cpp:99-200)
+    std::mt19937 rng(1102);
+    for (int it = 0; it < 25; ++it) {
+        const int L = it == 0 ? 1 : 1 + (int)(rng() % 300);
+        const int max_seq = L + (int)(rng() % 32);
+        const int hkv = 1 + (int)(rng() % 3);
+        const int g = 1 + (int)(rng() % 5);
+        const int hq = hkv * g;
+        const int d = it % 3 == 0 ? 128 : 16 * (1 + (int)(rng() % 4));
+        auto q = random_half(rng, (size_t)hq * d, -1, 1);
+        auto k = random_half(rng, (size_t)hkv * max_seq * d, -1, 1);
+        auto v = random_half(rng, (size_t)hkv * max_seq * d, -1, 1);
+        auto dq = upload(q), dk = upload(k), dv = upload(v);
+        DeviceBuffer<half> out((size_t)hq * d);
+        hip::decode_gqa(dq.data(), dk.data(), dv.data(), out.data(), L, hq, hkv, max_seq, d);
+        HIP_CHECK(hipDeviceSynchronize());
+        std::vector<float> ref((size_t)hq * d);
+        const int32_t len = L;
+        kvo_decode_attention(to_float(q).data(), to_float(k).data(), to_float(v).data(), &len,
+                             ref.data(), 1, hq, hkv, d, max_seq, 1);
+        char what[96];
+        std::snprintf(what, sizeof what, "decode_gqa shape %d (L=%d hq=%d hkv=%d d=%d)", it, L, hq, hkv, d);
+        check_close(download(out), ref, what);
+    }
+}
+
+void case_decode_gqa_split() {
+    // 25 random batched shapes (test_attention.cpp:34-183): group size 7
+    // every third shape, lengths 1, 17, 513 and random; with the reference's
+    // 8-split buffer and with the library workspace
+    std::mt19937 rng(1701);
+    for (int it = 0; it < 25; ++it) {
+        const int b = it % 4 == 0 ? 1 : 1 + (int)(rng() % 3);
+        const int hkv = 2;
+        const int g = it % 3 == 0 ? 7 : 1 + (int)(rng() % 7);
+        const int hq = hkv * g;
+        const int d = it % 2 ? 64 : 128;
+        std::vector<int> lens(b);
+        int max_seq = 0;
+        for (int i = 0; i < b; ++i) {
+            lens[i] = it == 0 ? 1 : it == 1 ? 17 : it == 2 ? 513 : 1 + (int)(rng() % 2000);
+            max_seq = std::max(max_seq, lens[i]);
+        }
+        auto q = random_half(rng, (size_t)b * hq * d, -1, 1);
+        auto k = random_half(rng, (size_t)b * hkv * max_seq * d, -1, 1);
+        auto v = random_half(rng, (size_t)b * hkv * max_seq * d, -1, 1);
+        auto dq = upload(q), dk = upload(k), dv = upload(v);
+        auto dl = upload(lens);
+        DeviceBuffer<half> out((size_t)b * hq * d), out2((size_t)b * hq * d);
+        DeviceBuffer<float> split(hip::decode_split_buffer_floats(b, hq, d));
+        const auto kv = hip::contiguous_view(dk.data(), hkv, max_seq, d);
+        const auto vv = hip::contiguous_view(dv.data(), hkv, max_seq, d);
+        hip::decode_gqa_split(dq.data(), kv, vv, dl.data(), out.data(), b, hq, hkv, d, max_seq,
+                              split.data());
+        hip::decode_gqa_split(dq.data(), kv, vv, dl.data(), out2.data(), b, hq, hkv, d, max_seq);
+        HIP_CHECK(hipDeviceSynchronize());
+        std::vector<float> ref((size_t)b * hq * d);
+        kvo_decode_attention(to_float(q).data(), to_float(k).data(), to_float(v).data(),
+                             lens.data(), ref.data(), b, hq, hkv, d, max_seq, 4);
+        char what[96];
+        std::snprintf(what, sizeof what, "split_buffer shape %d (b=%d g=%d d=%d L0=%d)", it, b, g, d, lens[0]);
+        check_close(download(out), ref, what);
+        std::snprintf(what, sizeof what, "library workspace shape %d", it);
+        check_close(download(out2), ref, what);
+    }
+}
+
+void case_flash_prefill_gqa() {
+    // 25 random shapes (test_attention.cpp:188-291): S = 1, 15, 17, 65 and
+    // random, group size 7 every third shape, D = 64 and 128, batch 1..2
+    std::mt19937 rng(1702);
+    for (int it = 0; it < 25; ++it) {
+        const int b = it % 5 == 4 ? 2 : 1;
+        const int hkv = 2;
+        const int g = it % 3 == 0 ? 7 : 1 + (int)(rng() % 7);
+        const int hq = hkv * g;
+        const int d = it % 2 ? 64 : 128;
+        const int S = it == 0 ? 1 : it == 1 ? 15 : it == 2 ? 17 : it == 3 ? 65 : 1 + (int)(rng() % 300);
+        auto q = random_half(rng, (size_t)b * S * hq * d, -1, 1);
+        auto k = random_half(rng, (size_t)b * S * hkv * d, -1, 1);
+        auto v = random_half(rng, (size_t)b * S * hkv * d, -1, 1);
+        auto dq = upload(q), dk = upload(k), dv = upload(v);
+        DeviceBuffer<half> out(q.size());
+        hip::flash_prefill_gqa(dq.data(), dk.data(), dv.data(), out.data(), S, hq, hkv, d, b);
+        HIP_CHECK(hipDeviceSynchronize());
+        const auto qf = to_float(q), kf = to_float(k), vf = to_float(v);
+        std::vector<float> ref(q.size());
+        for (int s = 0; s < b; ++s)
+            kvo_causal_gqa_rows(qf.data() + (size_t)s * S * hq * d, kf.data() + (size_t)s * S * hkv * d,
+                                vf.data() + (size_t)s * S * hkv * d, ref.data() + (size_t)s * S * hq * d,
+                                S, hq, hkv, d, 0, S, 4);
+        char what[96];
+        std::snprintf(what, sizeof what, "flash_prefill shape %d (b=%d S=%d g=%d d=%d)", it, b, S, g, d);
+        check_close(download(out), ref, what);
+    }
+}
+
+void case_causal_gqa() {
+    // the naive reference op is routed to the flash kernel: same results
+    std::mt19937 rng(1703);
+    const int S = 77, hq = 8, hkv = 2, d = 48;  // D outside the MFMA path
+    auto q = random_half(rng, (size_t)S * hq * d, -1, 1);
+    auto k = random_half(rng, (size_t)S * hkv * d, -1, 1);
+    auto v = random_half(rng, (size_t)S * hkv * d, -1, 1);
+    auto dq = upload(q), dk = upload(k), dv = upload(v);
+    DeviceBuffer<half> out(q.size());
+    hip::causal_gqa(dq.data(), dk.data(), dv.data(), out.data(), S, hq, hkv, d);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<float> ref(q.size());
+    kvo_causal_gqa(to_float(q).data(), to_float(k).data(), to_float(v).data(), ref.data(), S, hq, hkv, d);
+    check_close(download(out), ref, "causal_gqa");
+}
+
+void case_paged_identity_equals_kvcache() {
+    // One sequence whose pages are taken in order from a fresh pool has the
+    // identity block table, so the paged pool and KVCache's head-major block
+    // must hold the same bytes after the same appends.
+    std::mt19937 rng(1704);
+    const int layers = 2, hkv = 4, d = 64, max_seq = 96;
+    KVCache flat(layers, hkv, d, max_seq);
+    PagedKVCache paged(layers, hkv, d, max_seq / 16, 1, max_seq / 16);
+    const int slot = paged.add_sequence();
+    EXPECT(slot == 0, "first slot %d", slot);
+    int pos = 0;
+    for (int chunk : {37, 1, 1, 20, 5}) {
+        paged.begin_prefill(1, chunk);
+        paged.sync();
+        for (int l = 0; l < layers; ++l) {
+            auto ks = random_half(rng, (size_t)chunk * hkv * d, -2, 2);
+            auto vs = random_half(rng, (size_t)chunk * hkv * d, -2, 2);
+            auto dk = upload(ks), dv = upload(vs);
+            hip::append_kv_cache(dk.data(), dv.data(), flat.get_layer_ptr(l, 0),
+                                 flat.get_layer_ptr(l, 1), chunk, pos, hkv, max_seq, d);
+            paged.append(l, dk.data(), dv.data(), 1, chunk);
+            HIP_CHECK(hipDeviceSynchronize());
+        }
+        pos += chunk;
+    }
+    EXPECT(paged.seq_len(0) == pos, "length %d vs %d", paged.seq_len(0), pos);
+    for (int i = 0; i < paged.pages_used(0); ++i)
+        EXPECT(paged.host_block_table(0)[i] == i, "page %d -> %d", i, paged.host_block_table(0)[i]);
+    for (int l = 0; l < layers; ++l)
+        for (int kv = 0; kv < 2; ++kv) {
+            std::vector<half> a((size_t)hkv * max_seq * d), p(a.size());
+            HIP_CHECK(hipMemcpy(a.data(), flat.get_layer_ptr(l, kv), a.size() * 2, hipMemcpyDeviceToHost));
+            HIP_CHECK(hipMemcpy(p.data(), paged.get_layer_ptr(l, kv), p.size() * 2, hipMemcpyDeviceToHost));
+            EXPECT(bits_equal(a, p), "layer %d %s differs", l, kv ? "V" : "K");
+        }
+}
+
+void case_paged_serving_steps() {
+    // Runner flow over PagedKVCache: prefill three sequences (K/V written to
+    // pages by the prefill kernel), then decode steps with "bump, then write
+    // at num_tokens - 1"; every step's attention is checked against the oracle
+    // over the full history, and a freed sequence's pages are reused.
+    std::mt19937 rng(1705);
+    const int hq = 8, hkv = 2, d = 128, B = 3, steps = 4;
+    const int prompt[B] = {40, 17, 90};
+    PagedKVCache cache(1, hkv, d, 64, B, 16);
+    std::vector<std::vector<half>> hist_k(B), hist_v(B);  // [t][hkv][d] per sequence
+    for (int s = 0; s < B; ++s) {
+        EXPECT(cache.add_sequence() == s, "slot %d", s);
+        const int S = prompt[s];
+        auto q = random_half(rng, (size_t)S * hq * d, -1, 1);
+        hist_k[s] = random_half(rng, (size_t)S * hkv * d, -1, 1);
+        hist_v[s] = random_half(rng, (size_t)S * hkv * d, -1, 1);
+        cache.reserve(s, S);
+        cache.set_seq_len(s, S);
+        cache.sync();
+        auto dq = upload(q), dk = upload(hist_k[s]), dv = upload(hist_v[s]);
+        DeviceBuffer<half> out(q.size());
+        // one sequence's own block-table row
+        hip::flash_prefill_gqa_paged(dq.data(), dk.data(), dv.data(), out.data(), S, hq, hkv, d, 1,
+                                     cache.get_layer_ptr(0, 0), cache.get_layer_ptr(0, 1),
+                                     cache.block_tables() + (size_t)s * cache.max_pages_per_seq(),
+                                     cache.max_pages_per_seq(), cache.num_pages());
+        HIP_CHECK(hipDeviceSynchronize());
+        std::vector<float> ref(q.size());
+        kvo_causal_gqa_rows(to_float(q).data(), to_float(hist_k[s]).data(), to_float(hist_v[s]).data(),
+                            ref.data(), S, hq, hkv, d, 0, S, 4);
+        check_close(download(out), ref, "paged prefill");
+    }
+    auto run_steps = [&](int nsteps) {
+        for (int st = 0; st < nsteps; ++st) {
+            cache.begin_decode_step(B);
+            cache.sync();
+            auto q = random_half(rng, (size_t)B * hq * d, -1, 1);
+            auto kn = random_half(rng, (size_t)B * hkv * d, -1, 1);
+            auto vn = random_half(rng, (size_t)B * hkv * d, -1, 1);
+            auto dq = upload(q), dk = upload(kn), dv = upload(vn);
+            DeviceBuffer<half> out(q.size());
+            int max_len = 0;
+            for (int s = 0; s < B; ++s) max_len = std::max(max_len, cache.seq_len(s));
+            cache.append(0, dk.data(), dv.data(), B, 1);
+            cache.decode(0, dq.data(), out.data(), B, hq, max_len);
+            HIP_CHECK(hipDeviceSynchronize());
+            // oracle over the contiguous history [B][hkv][max_len][d]
+            std::vector<float> kc((size_t)B * hkv * max_len * d, 0.f), vc(kc.size(), 0.f);
+            std::vector<int32_t> lens(B);
+            for (int s = 0; s < B; ++s) {
+                hist_k[s].insert(hist_k[s].end(), kn.begin() + (size_t)s * hkv * d, kn.begin() + (size_t)(s + 1) * hkv * d);
+                hist_v[s].insert(hist_v[s].end(), vn.begin() + (size_t)s * hkv * d, vn.begin() + (size_t)(s + 1) * hkv * d);
+                lens[s] = cache.seq_len(s);
+                EXPECT((size_t)lens[s] * hkv * d == hist_k[s].size(), "history length of %d", s);
+                for (int t = 0; t < lens[s]; ++t)
+                    for (int h = 0; h < hkv; ++h)
+                        for (int i = 0; i < d; ++i) {
+                            const size_t dst = (((size_t)s * hkv + h) * max_len + t) * d + i;
+                            const size_t src = ((size_t)t * hkv + h) * d + i;
+                            kc[dst] = half_to_float(hist_k[s][src]);
+                            vc[dst] = half_to_float(hist_v[s][src]);
+                        }
+            }
+            std::vector<float> ref(q.size());
+            kvo_decode_attention(to_float(q).data(), kc.data(), vc.data(), lens.data(), ref.data(),
+                                 B, hq, hkv, d, max_len, 4);
+            char what[64];
+            std::snprintf(what, sizeof what, "paged decode step (lens %d,%d,%d)", lens[0], lens[1], lens[2]);
+            check_close(download(out), ref, what);
+        }
+    };
+    run_steps(steps);
+    // sequence 1 finishes; a new one takes its slot and reuses its pages
+    const int freed = cache.pages_used(1);
+    const int before = cache.free_page_count();
+    cache.release(1);
+    EXPECT(cache.free_page_count() == before + freed, "pages not returned");
+    EXPECT(cache.add_sequence() == 1, "slot reuse");
+    hist_k[1].clear();
+    hist_v[1].clear();
+    {
+        const int S = 33;
+        hist_k[1] = random_half(rng, (size_t)S * hkv * d, -1, 1);
+        hist_v[1] = random_half(rng, (size_t)S * hkv * d, -1, 1);
+        cache.set_seq_len(1, S);
+        cache.sync();
+        std::vector<int32_t> zero_pos(B, 0);
+        auto dk = upload(hist_k[1]), dv = upload(hist_v[1]);
+        DeviceBuffer<int32_t> pos = upload(zero_pos);
+        hip::paged_append_kv(dk.data(), dv.data(), cache.get_layer_ptr(0, 0), cache.get_layer_ptr(0, 1),
+                             cache.block_tables() + (size_t)cache.max_pages_per_seq(),
+                             cache.max_pages_per_seq(), pos.data(), 1, S, hkv, d, cache.num_pages());
+        HIP_CHECK(hipDeviceSynchronize());
+    }
+    run_steps(2);
+    // the gather of every sequence reproduces its history bit for bit
+    int max_len = 0;
+    std::vector<int32_t> lens(B);
+    for (int s = 0; s < B; ++s) max_len = std::max(max_len, lens[s] = cache.seq_len(s));
+    DeviceBuffer<half> gk((size_t)B * hkv * max_len * d), gv(gk.size());
+    DeviceBuffer<int32_t> dl = upload(lens);
+    hip::paged_gather_kv(cache.get_layer_ptr(0, 0), cache.get_layer_ptr(0, 1), cache.block_tables(),
+                         cache.max_pages_per_seq(), dl.data(), B, hkv, d, cache.num_pages(), max_len,
+                         gk.data(), gv.data());
+    HIP_CHECK(hipDeviceSynchronize());
+    auto hk = download(gk);
+    bool same = true;
+    for (int s = 0; s < B; ++s)
+        for (int t = 0; t < lens[s]; ++t)
+            for (int h = 0; h < hkv; ++h)
+                same &= std::memcmp(&hk[(((size_t)s * hkv + h) * max_len + t) * d],
+                                    &hist_k[s][((size_t)t * hkv + h) * d], d * 2) == 0;
+    EXPECT(same, "gathered K differs from the appended history");
+}
+
+struct Case {
+    const char* name;
+    bool gpu;
+    void (*fn)();
+};
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const bool gpu = argc > 1 && std::strcmp(argv[1], "--gpu") == 0;
+    const bool cpu = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+    if (!gpu && !cpu) {
+        std::fprintf(stderr, "usage: %s --cpu | --gpu\n", argv[0]);
+        return 2;
+    }
+    const Case cases[] = {
+        {"half_conversion", false, case_half_conversion},
+        {"host_validation", false, case_host_validation},
+        {"kv_cache_layout", true, case_kv_cache_layout},
+        {"append_kv_cache", true, case_append_kv_cache},
+        {"decode_gqa", true, case_decode_gqa},
+        {"decode_gqa_split", true, case_decode_gqa_split},
+        {"flash_prefill_gqa", true, case_flash_prefill_gqa},
+        {"causal_gqa", true, case_causal_gqa},
+        {"paged_identity_equals_kvcache", true, case_paged_identity_equals_kvcache},
+        {"paged_serving_steps", true, case_paged_serving_steps},
+    };
+    for (const Case& c : cases) {
+        if (c.gpu && !gpu) continue;
+        g_case = c.name;
+        const int before = g_failures;
+        std::printf("case %s ...\n", c.name);
+        std::fflush(stdout);
+        try {
+            c.fn();
+        } catch (const std::exception& e) {
+            ++g_failures;
+            std::printf("  FAIL [%s] exception: %s\n", c.name, e.what());
+        }
+        std::printf("case %s: %s\n", c.name, g_failures == before ? "ok" : "FAILED");
+        std::fflush(stdout);
+    }
+    std::printf("%d checks, %d failures\n", g_checks, g_failures);
+    return g_failures ? 1 : 0;
+}

@@ -33,23 +33,33 @@ def test_kv_view_struct_layout_matches_header():
 
 
 def test_auto_split_policy():
-    # page-aligned chunks of >= 64 tokens, never more than 1024 splits
+    # chunks of ~L/64 tokens but >= 128 (64-token multiples), grid of at most
+    # 6144 workgroups, never more than 256 splits
     assert kvhp.decode_auto_splits(1, 8, 128, 64) == 1
-    for b, hkv, L in [(1, 8, 512), (1, 8, 4096), (1, 8, 65536), (32, 8, 8192), (1, 4, 2176)]:
+    expect = {(1, 8, 4096): 32, (1, 8, 16384): 64, (1, 8, 65536): 64, (1, 4, 2176): 17,
+              (1, 8, 512): 4, (32, 8, 8193): 22}
+    for (b, hkv, L), want in expect.items():
+        assert kvhp.decode_auto_splits(b, hkv, 128, L) == want, (b, hkv, L)
+    for b, hkv, L in [(1, 8, 100), (3, 2, 600), (64, 8, 32768), (1, 1, 1 << 20), (256, 32, 4096)]:
         s = kvhp.decode_auto_splits(b, hkv, 128, L)
-        assert 1 <= s <= 1024
+        assert 1 <= s <= 256
+        assert s == 1 or b * hkv * s <= 6144
         chunk = -(-L // s)
-        assert s <= -(-L // 64)
-        assert b * hkv * s >= min(4096, b * hkv * -(-L // 64)) // 2 or chunk <= 128
+        assert s == 1 or chunk >= 64
 
 
 def test_workspace_sizing():
     # no workspace when a single split covers the sequence
     assert kvhp.decode_workspace_bytes(1, 32, 8, 128, 64, 1) == 0
-    n = kvhp.decode_workspace_bytes(2, 32, 8, 128, 4096, 16)
-    # tickets (2*8 u32) + partial o (2*32*16*128 f32) + (m,l) pairs, 256-B aligned
-    assert n >= 2 * 32 * 16 * (128 + 2) * 4 + 2 * 8 * 4
-    assert n % 256 == 0
+    # splits * B * Hq * (D + 2) floats, never more than the split_buffer the
+    # reference's callers allocate for that split count (test_attention.cpp:124,
+    # forward_gpu.cu:100); a request is rounded to 64-token chunks, so 8
+    # splits of 600 tokens become 5 chunks of 128
+    for b, hq, hkv, d, L, s, used in [(2, 32, 8, 128, 4096, 16, 16), (3, 14, 2, 64, 600, 8, 5),
+                                      (1, 32, 4, 64, 2176, 0, None)]:
+        n = kvhp.decode_workspace_bytes(b, hq, hkv, d, L, s)
+        used = used or kvhp.decode_auto_splits(b, hkv, d, L)
+        assert n == used * b * hq * (d + 2) * 4
 
 
 def _null_view():
