@@ -12,7 +12,7 @@
  * tests pass them (tests/test_attention.cpp:75-77); KV movement works on raw
  * 16-bit patterns so "bit-exact" is literal.
  *
- * Pinning (how each function is checked, see tests/test_oracle_*.py):
+ * Pinning (how each function is checked, see tests/test_oracle.py):
  *   kvo_causal_gqa       bit-exact vs the reference src/cpu/ops.cpp compiled
  *                        under oracle/_ref, golden fixtures, KAT row0 == v[0]
  *   kvo_decode_attention == last row of kvo_causal_gqa (invariant), KATs

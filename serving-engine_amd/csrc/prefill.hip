@@ -1,32 +1,38 @@
 // prefill.hip -- causal flash attention for prefill on CDNA4 fp16 MFMA (gfx950).
 //
-// Work decomposition: a 256-thread workgroup (4 waves) owns one KV head and
+// Work decomposition: a 512-thread workgroup (8 waves) owns one KV head and
 // a query block of 16*RB rows for all G query heads of that KV head -- G*RB
-// units of (head, 16 rows), two units per wave (RB = 8/G).  Each 64-key K/V
-// tile is loaded from HBM once, staged in double-buffered LDS, and consumed
-// by every unit, so GQA heads share their K/V traffic.  Query blocks i and
-// N-1-i are processed by the same workgroup, giving every workgroup the same
-// causal work; grid x enumerates (pair, kv_head) with the kv head fastest so
-// a kv head's workgroups land on one XCD (8 KV heads -> x % 8).
+// = 8 units of (head, 16 rows), one unit per wave (RB = 8/G).  Each 64-key
+// K/V tile is read from HBM once per workgroup and consumed by all 8 waves,
+// so GQA heads share their K/V traffic.  Query blocks i and N-1-i are
+// processed by the same workgroup, giving every workgroup the same causal
+// work; grid x enumerates (pair, kv_head) with the kv head fastest.
+//
+// K/V staging: a 4-stage LDS ring (4 x 32 KB for D=128), filled by
+// global_load_lds_dwordx4 (direct HBM->LDS, no VGPR round trip).  Tile t+3 is
+// issued while tile t is consumed; before reading a stage each wave waits for
+// its own loads of that stage (explicit s_waitcnt vmcnt(N)) and the
+// workgroup meets at one barrier per tile.  Rows are stored with an XOR
+// swizzle of their 16-byte chunks so that both the K reads (ds_read_b128)
+// and the transposing V reads (ds_read_b64_tr_b16) are bank-conflict free.
 //
 // Per tile and unit, the contraction runs transposed so that one lane owns one
 // query row for the whole online softmax:
-//   S^T = K Q^T     v_mfma_f32_16x16x32_f16, A = K rows (ds_read_b128 from
-//                   LDS, shared by both units), B = Q^T held in registers.
-//                   Lane l gets keys 4(l/16)+e of each 16-key block for query
-//                   row l%16.
+//   S^T = K Q^T     v_mfma_f32_16x16x32_f16, A = K rows from LDS, B = Q^T
+//                   held in registers.  Lane l gets keys 4(l/16)+e of each
+//                   16-key block for query row l%16.
 //   softmax         fp32 in the log2 domain; the causal mask is applied only on
-//                   tiles that cross the diagonal; fully masked units skip.
+//                   tiles that cross the diagonal; the running max is taken on
+//                   raw scores and the rescale of O is skipped when no row's
+//                   max moved.
 //   O^T += V^T P^T  A = V^T read with ds_read_b64_tr_b16 (transposing 8-byte
 //                   LDS reads), B = P^T converted to fp16 straight from the S^T
 //                   accumulators: k-slot (g,e') of a 32-key step is key
 //                   4g+e' (e'<4) or 16+4g+e'-4 in both operands.
-// The next tile's global loads are issued before the current tile's MFMAs and
-// written to the other LDS buffer afterwards: one barrier per tile.
 //
 // With a page pool, each workgroup also writes the K/V rows of its own query
-// block into the pages from the registers it already loaded (every key row is
-// written exactly once, bit-exact).
+// block into the pages after its outputs (every key row is written exactly
+// once, bit-exact).
 //
 // Roofline: MFMA-bound for long prompts; algorithmic work 4*D*Hq*S(S+1)/2
 // flops (the two causal contractions).
