@@ -1,33 +1,33 @@
 // decode.hip -- split-K decode attention over a GQA fp16 KV cache (gfx950).
 //
 // Work decomposition: one 64-lane workgroup per (split, kv_head, sequence).
-// A split is a page-aligned chunk of `chunk` tokens (a multiple of 64); the
-// workgroup serves all G = Hq/Hkv query heads of its KV head, so every K/V
-// byte is read from HBM exactly once (the reference re-reads each KV row once
-// per query head, src/cuda/decode_attention_split.cu:40-49).
+// A split is a page-aligned chunk of `chunk` tokens (a multiple of 64; at
+// most 64 pages with a block table); the workgroup serves all G = Hq/Hkv
+// query heads of its KV head, so every K/V byte is read from HBM exactly once
+// (the reference re-reads each KV row once per query head,
+// src/cuda/decode_attention_split.cu:40-49).
 //
-// Per 64-token iteration (4 pages of 16 tokens), both contractions run on
-// v_mfma_f32_16x16x32_f16:
-//   S = Q K^T   A = Q (row r holds head r % CG), B = K^T loaded straight from
-//               HBM: lane l holds 16 B of token (page t, slot l%16) at dims
-//               32c + 8(l/16), i.e. 64 contiguous bytes per row.  Lane l keeps
-//               the tile that belongs to it, so the 64 lanes hold 64 tokens x 4
-//               heads each with no redundancy.
-//   softmax     fp32, log2 domain (scores pre-scaled by log2(e)/sqrt(D)); the
-//               running max per head is a DPP row reduction + 2 swizzles.  Each
-//               lane's heads are the same rows it owns in the O accumulator, so
-//               the rescale factor never leaves the lane.
-//   O += P V    A = P (fp16) and B = V^T, both read from this wave's LDS tiles
-//               with ds_read_b64_tr_b16 (transposing 8-byte reads); V arrives
-//               from HBM as whole 256 B rows (1 KiB per wave load) and is
-//               written to LDS row-major.
-// K and V live in a two-deep register ring: iteration i+2 is fetched while
-// iteration i computes, with identical loads on every path so the compiler
-// keeps exact vmcnt waits (no pipeline drain).
+// Per 32-token step (2 pages of 16 tokens), both contractions run on
+// v_mfma_f32_16x16x32_f16 in transposed form, so that lane (g, col) owns
+// query head `col` for the whole online softmax:
+//   S^T = K Q^T     A = K rows loaded straight from HBM (lane: token col of
+//                   a page, 16 B at dims 32c + 8g), B = Q^T held in
+//                   registers (zero columns for heads >= G).
+//   softmax         fp32 in the log2 domain; per-lane max over its 8 tokens,
+//                   then v_permlane16/32_swap across the four lane rows (no
+//                   LDS round trip); the rescale factor never leaves the lane
+//                   and O is rescaled only when some head's max moved.
+//   O^T += V^T P^T  A = V^T read from a padded LDS tile with
+//                   ds_read_b64_tr_b16 (transposing 8-byte reads), B = P^T in
+//                   fp16 straight from the S^T accumulators.
+// K is fetched two steps ahead into registers and V one step ahead (V goes
+// through LDS for the transposed reads), with non-temporal loads (the cache
+// is streamed once) and identical loads on every path so the compiler keeps
+// exact vmcnt waits.  246 VGPRs at D=128: two waves per SIMD.
 //
 // Splits: a sequence whose keys fit one split gets its output written
 // directly; otherwise each split stores (m, l, o[D]) in fp32 and
-// decode_merge_kernel (a second, tiny launch) combines them by log-sum-exp.
+// decode_merge_kernel (a second, small launch) combines them by log-sum-exp.
 //
 // Roofline: HBM-bound; algorithmic bytes per (token, kv_head) are 4*D
 // (K + V fp16) plus the q read and output write per query head.
@@ -42,8 +42,9 @@ namespace kvhp {
 
 namespace {
 
-constexpr int kMaxSplits = 256;   // partials per (sequence, kv head)
-constexpr int kTok = 64;          // tokens per pipelined iteration (4 pages)
+constexpr int kMaxSplits = 512;   // partials per (sequence, kv head)
+constexpr int kMaxPagedChunk = 1024;  // tokens per split with a block table: one
+                                      // page id per lane of a wave (64 pages)
 
 struct KVDev {
     const f16* data;
@@ -90,31 +91,49 @@ __device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
     return __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-template <int G>
-struct Groups {
-    static constexpr int CG = G <= 4 ? 4 : (G <= 8 ? 8 : 16);  // heads per MFMA row set
-    static constexpr int R = CG / 4;                             // lane head groups
-};
+// Max / sum across the four 16-lane rows of a wave with the gfx950 row
+// swaps (VALU only, no LDS round trip).  Rows 0<->1, 2<->3, then 01<->23.
+__device__ __forceinline__ float rows4_max(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
 
+// One 64-lane workgroup per (split, kv_head, sequence).  Both contractions
+// are transposed so that lane (g, col) -- g = lane/16, col = lane%16 -- owns
+// query head `col` of the KV head's group for the whole online softmax:
+//   S^T = K Q^T   A = K rows of one 16-token page (lane: token col, dims
+//                 32c+8g..+8, 64 contiguous bytes per row), B = Q^T (lane:
+//                 head col, same dims; zero for col >= G).  Lane (g, col)
+//                 gets tokens 4g+e of the page for head col.
+//   softmax       per head = per lane: in-lane max over its 8 tokens of the
+//                 32-token step, then rows4_max; rescale factor lane-local.
+//   O^T += V^T P^T  A = V^T from LDS by transposing 8-byte reads (dims
+//                 16db+col, tokens 4g..4g+3 and 16+4g..16+4g+3), B = P^T in
+//                 fp16 straight from the S^T accumulators (k-slot (g, e) is
+//                 token 4g+e of page 0 for e < 4, of page 1 for e >= 4).
+// K runs two steps ahead in registers, V one step (it is staged through LDS
+// for the transposed reads).
 template <int D, int G, bool PAGED>
-__global__ void __launch_bounds__(kWave)
+__global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_splitk_kernel(const DecodeArgs a) {
-    constexpr int TOK = kTok;
-    constexpr int CG = Groups<G>::CG;
-    constexpr int R = Groups<G>::R;
-    constexpr int NC = D / 32;       // MFMA k-chunks of the QK contraction
-    constexpr int ND = D / 16;       // 16-dim blocks of the output
+    static_assert(G >= 1 && G <= 16, "one MFMA column per query head");
+    constexpr int TOK = 32;          // tokens per step: 2 pages, one PV k-step
+    constexpr int NC = D / 32;       // QK k-chunks
+    constexpr int ND = D / 16;       // 16-dim output blocks
     constexpr int LPR = D / 8;       // lanes per V row (16 B each)
     constexpr int RPL = kWave / LPR; // V rows per wave load
-    constexpr int NVL = TOK / RPL;   // V loads per iteration
-    constexpr int NT = TOK / 16;     // 16-token pages per iteration
-    constexpr int TPR = 4 / R;       // tiles per score round
-    constexpr int NR = NT / TPR;     // score rounds per iteration
+    constexpr int NVL = TOK / RPL;   // V loads per step
     constexpr int VP = D + 16;       // V tile row pitch in halfs (bank skew)
-    constexpr int REP = 4 / R;       // lane groups holding the same heads
 
     __shared__ __attribute__((aligned(16))) f16 v_lds[TOK * VP];
-    __shared__ __attribute__((aligned(16))) f16 p_lds[TOK * CG];
 
     const int lane = threadIdx.x;
     const int g = lane >> 4;
@@ -123,6 +142,21 @@ decode_splitk_kernel(const DecodeArgs a) {
     const int kvh = blockIdx.y;
     const int b = blockIdx.z;
     const int64_t row0 = (int64_t)b * a.Hq + (int64_t)kvh * G;  // first q row
+    const bool hvalid = col < G;
+
+    // Page ids of this split, one per lane (the host keeps a paged split to
+    // at most 64 pages): one vector load here instead of a scalar load per
+    // step on the critical path; steps fetch them with v_readlane.
+    int pidv = 0;
+    const int first_page = (split * a.chunk) >> 4;
+    if constexpr (PAGED) {
+        const int32_t* row = a.k.bt + (int64_t)b * a.k.max_pages;
+        const int in_row = a.k.max_pages - first_page;
+        if (in_row > 0) {
+            int pid = row[first_page + (lane < in_row ? lane : in_row - 1)];
+            pidv = pid < 0 ? 0 : (pid >= a.k.num_pages ? a.k.num_pages - 1 : pid);
+        }
+    }
 
     int L = seq_len_of(a, b);
     if (L > a.cap) L = a.cap;
@@ -139,8 +173,6 @@ decode_splitk_kernel(const DecodeArgs a) {
     const int t_begin = split * a.chunk;
     const int t_end = min(L, t_begin + a.chunk);
     const int n_iter = (t_end - t_begin + TOK - 1) / TOK;
-    // Loads never leave this split: rows past its end re-read its last row
-    // (a cache hit), so prefetches can be issued unconditionally.
     const int last_tok = t_end - 1;
     const int last_pi = last_tok >> 4;
     const int last_slot = last_tok & 15;
@@ -148,173 +180,150 @@ decode_splitk_kernel(const DecodeArgs a) {
     const int64_t ssk = a.k.stride_s, ssv = a.v.stride_s;
     const f16* kbase;
     const f16* vbase;
-    const int32_t* bt = nullptr;
-    if constexpr (PAGED) {
+    if constexpr (PAGED) {  // K and V share one block table
         kbase = a.k.data + kvh * a.k.stride_h;
         vbase = a.v.data + kvh * a.v.stride_h;
-        bt = a.k.bt + (int64_t)b * a.k.max_pages;  // K and V share one table
     } else {
         kbase = a.k.data + b * a.k.stride_b + kvh * a.k.stride_h;
         vbase = a.v.data + b * a.v.stride_b + kvh * a.v.stride_h;
     }
 
-    // A operand of QK: lane l holds q[head (l%16) % CG][dims 32c + 8(l/16) .. +8].
-    half8 qa[NC];
-    {
-        const int hq = col % CG;
-        if (hq < G) {
-            const f16* qp = a.q + (row0 + hq) * D + 8 * g;
+    // B operand of S^T: lane (g, col) holds q[head col][dims 32c + 8g .. +8].
+    half8 qb[NC];
+    if (hvalid) {
+        const f16* qp = a.q + (row0 + col) * D + 8 * g;
 #pragma unroll
-            for (int c = 0; c < NC; ++c) qa[c] = load_half8(qp + 32 * c);
-        } else {
+        for (int c = 0; c < NC; ++c) qb[c] = load_half8(qp + 32 * c);
+    } else {
 #pragma unroll
-            for (int c = 0; c < NC; ++c) qa[c] = half8{};
-        }
+        for (int c = 0; c < NC; ++c) qb[c] = half8{};
     }
 
     const int vrow = lane / LPR;
     const int vdim = 8 * (lane % LPR);
 
-    // Physical row offset (in units of rows) of each page of the iteration
-    // starting at T0; pages past the split clamp to its last page.  Uniform
-    // across the wave, so these are scalar loads.
-    auto page_rows = [&](int T0, int64_t (&pr)[NT]) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int pi = min((T0 >> 4) + t, last_pi);
-            if constexpr (PAGED) {
-                int pid = bt[pi];
-                pid = pid < 0 ? 0 : (pid >= a.k.num_pages ? a.k.num_pages - 1 : pid);
-                pr[t] = (int64_t)pid * kPage;
-            } else {
-                pr[t] = (int64_t)pi * kPage;
-            }
-        }
+    // Page t of the step starting at T0, clamped into the split: a
+    // wave-uniform base pointer, plus the last row a lane may read in it
+    // (rows past the split's last token re-read its last row, so every load
+    // is in bounds and finite, and prefetches are unconditional).  Lane
+    // offsets inside a page are 32-bit: one saddr + voffset load each.
+    auto page_base = [&](const f16* base, int64_t ss, int T0, int t, int& lim) {
+        const int pu = (T0 >> 4) + t;
+        const int pi = min(pu, last_pi);
+        lim = pu >= last_pi ? last_slot : kPage - 1;
+        int64_t row;
+        if constexpr (PAGED)
+            row = (int64_t)__builtin_amdgcn_readlane(pidv, pi - first_page) * kPage;
+        else
+            row = (int64_t)pi * kPage;
+        return reinterpret_cast<const char*>(base + row * ss);
     };
 
-    half8 kbuf[2][NT][NC];
-    half8 vbuf[2][NVL];
+    half8 kbuf[2][2][NC];  // [ring slot][page][k-chunk]
+    half8 vbuf[NVL];
+    const uint32_t kss = static_cast<uint32_t>(ssk) * 2u;  // row pitch, bytes
+    const uint32_t vss = static_cast<uint32_t>(ssv) * 2u;
 
     auto load_k = [&](auto S_, int T0) {
         constexpr int S = decltype(S_)::value;
-        int64_t pr[NT];
-        page_rows(T0, pr);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int slot = (T0 + 16 * t + col <= last_tok) ? col : last_slot;
-            const f16* rp = kbase + (pr[t] + slot) * ssk + 8 * g;
+        for (int t = 0; t < 2; ++t) {
+            int lim;
+            const char* pb = page_base(kbase, ssk, T0, t, lim);
+            const uint32_t off = __umul24(static_cast<uint32_t>(min(col, lim)), kss) + 16u * g;
 #pragma unroll
-            for (int c = 0; c < NC; ++c) kbuf[S][t][c] = load_half8(rp + 32 * c);
+            for (int c = 0; c < NC; ++c)
+                kbuf[S][t][c] = load_half8_stream(reinterpret_cast<const f16*>(pb + off + 64 * c));
         }
     };
-    auto load_v = [&](auto S_, int T0) {
-        constexpr int S = decltype(S_)::value;
-        int64_t pr[NT];
-        page_rows(T0, pr);
+    auto load_v = [&](int T0) {
 #pragma unroll
-        for (int j = 0; j < NVL; ++j) {
-            const int t = (RPL * j) >> 4;
-            const int s0 = ((RPL * j) & 15) + vrow;
-            const int slot = (T0 + RPL * j + vrow <= last_tok) ? s0 : last_slot;
-            vbuf[S][j] = load_half8(vbase + (pr[t] + slot) * ssv + vdim);
+        for (int t = 0; t < 2; ++t) {
+            int lim;
+            const char* pb = page_base(vbase, ssv, T0, t, lim);
+#pragma unroll
+            for (int j = t * (kPage / RPL); j < (t + 1) * (kPage / RPL); ++j) {
+                const int s0 = ((RPL * j) & (kPage - 1)) + vrow;
+                const uint32_t off = __umul24(static_cast<uint32_t>(min(s0, lim)), vss) + 2u * vdim;
+                vbuf[j] = load_half8_stream(reinterpret_cast<const f16*>(pb + off));
+            }
         }
     };
 
-    float m_run[4], l_part[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        m_run[e] = -1e30f;
-        l_part[e] = 0.f;
-    }
-    floatx4 o[ND];
+    float m_run = -1e30f;  // running max of raw scores for head col
+    float l_part = 0.f;    // this lane's share of the softmax denominator
+    floatx4 o[ND];         // O^T: lane (g, col) holds dims 16db + 4g + e of head col
 #pragma unroll
     for (int db = 0; db < ND; ++db) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const float sc = a.scale_log2;
+    const f16* vrd = &v_lds[(4 * g + col / 4) * VP + 4 * (col % 4)];
 
-    // One iteration on ring slot S.  With PREFETCH the slot is refilled with
-    // iteration it+2 as soon as each half is consumed.
-    auto step = [&](auto S_, auto PF_, int it) {
+    auto step = [&](auto S_, auto PFK_, auto PFV_, int it) {
         constexpr int S = decltype(S_)::value;
-        constexpr bool PREFETCH = decltype(PF_)::value;
+        constexpr bool PFK = decltype(PFK_)::value;
+        constexpr bool PFV = decltype(PFV_)::value;
         const int T0 = t_begin + TOK * it;
 
-        // ---- S = Q K^T, one accumulator per 16-token page.
-        floatx4 C[NT];
+        // ---- S^T = K Q^T for the two pages of the step.
+        floatx4 C[2];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
+        for (int t = 0; t < 2; ++t) {
             C[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c)
-                C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kbuf[S][t][c], C[t], 0, 0, 0);
+                C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbuf[S][t][c], qb[c], C[t], 0, 0, 0);
         }
-        if constexpr (PREFETCH) load_k(S_, T0 + 2 * TOK);
+        if constexpr (PFK) load_k(S_, T0 + 2 * TOK);
 
-        // ---- the lane's own scores: heads 4*(g%R)+e of token 16*tile + col.
-        float s[NR][4];
-        int tile_of[NR];
+        // ---- tokens past the split (only in its last step).
+        if (T0 + TOK > t_end) {
 #pragma unroll
-        for (int rr = 0; rr < NR; ++rr) {
-            const int sub = g / R;
-            floatx4 sel = C[rr * TPR];
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int u = 1; u < TPR; ++u)
-                if (sub == u) sel = C[rr * TPR + u];
-            const int tile = rr * TPR + sub;
-            tile_of[rr] = tile;
-            const bool ok = T0 + 16 * tile + col < t_end;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s[rr][e] = ok ? sel[e] * a.scale_log2 : -INFINITY;
+                for (int e = 0; e < 4; ++e)
+                    if (T0 + 16 * t + 4 * g + e >= t_end) C[t][e] = -INFINITY;
         }
 
-        // ---- running max per head, rescale factor (lane-local heads).
-        float alpha[4];
+        // ---- running max of head col, rescale factor, P^T in fp16.
+        float mx = fmaxf(fmaxf(fmaxf(C[0][0], C[0][1]), fmaxf(C[0][2], C[0][3])),
+                         fmaxf(fmaxf(C[1][0], C[1][1]), fmaxf(C[1][2], C[1][3])));
+        mx = rows4_max(mx);
+        const float mn = fmaxf(m_run, mx);
+        const float alpha = fast_exp2((m_run - mn) * sc);
+        m_run = mn;
+        const float nm = hvalid ? -mn * sc : -INFINITY;  // padding heads get p = 0
+        half8 pt;
+        float ps = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float mt = s[0][e];
-#pragma unroll
-            for (int rr = 1; rr < NR; ++rr) mt = fmaxf(mt, s[rr][e]);
-            mt = row16_max(mt);
-            if constexpr (R == 1) mt = fmaxf(mt, __shfl_xor(mt, 16));
-            if constexpr (R <= 2) mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const float mn = fmaxf(m_run[e], mt);
-            alpha[e] = fast_exp2(m_run[e] - mn);
-            m_run[e] = mn;
-            l_part[e] *= alpha[e];
-        }
-
-        // ---- P (fp16) and V into this wave's LDS tiles.
-#pragma unroll
-        for (int rr = 0; rr < NR; ++rr) {
-            half4 ph;
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                ph[e] = static_cast<f16>(fast_exp2(s[rr][e] - m_run[e]));
-                l_part[e] += static_cast<float>(ph[e]);
+                const f16 ph = static_cast<f16>(fast_exp2(fmaf(C[t][e], sc, nm)));
+                pt[4 * t + e] = ph;
+                ps += static_cast<float>(ph);
             }
-            *reinterpret_cast<half4*>(&p_lds[(16 * tile_of[rr] + col) * CG + 4 * (g % R)]) = ph;
-        }
+        l_part = fmaf(l_part, alpha, ps);
+
+        // ---- V tile into LDS, then the next V tile into the registers.
 #pragma unroll
         for (int j = 0; j < NVL; ++j)
-            *reinterpret_cast<half8*>(&v_lds[(RPL * j + vrow) * VP + vdim]) = vbuf[S][j];
-        if constexpr (PREFETCH) load_v(S_, T0 + 2 * TOK);
+            *reinterpret_cast<half8*>(&v_lds[(RPL * j + vrow) * VP + vdim]) = vbuf[j];
+        if constexpr (PFV) load_v(T0 + TOK);
 
+        // Rescale O only when some head's running max moved.
+        if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.f)) {
 #pragma unroll
-        for (int db = 0; db < ND; ++db)
+            for (int db = 0; db < ND; ++db)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[db][e] *= alpha[e];
+                for (int e = 0; e < 4; ++e) o[db][e] *= alpha;
+        }
 
-        // ---- O += P V: k-slot (g, e') of step ks is token ks*32 + 8g + e'.
+        // ---- O^T += V^T P^T.
 #pragma unroll
-        for (int ks = 0; ks < TOK / 32; ++ks) {
-            const int trow = ks * 32 + 8 * g + col / 4;
-            const f16* pa = &p_lds[trow * CG + 4 * ((col % 4) % R)];
-            const half8 pop = cat_half8(lds_read_tr16(pa), lds_read_tr16(pa + 4 * CG));
-            const f16* pv = &v_lds[trow * VP + 4 * (col % 4)];
-#pragma unroll
-            for (int db = 0; db < ND; ++db) {
-                const half8 vop = cat_half8(lds_read_tr16(pv + 16 * db),
-                                            lds_read_tr16(pv + 16 * db + 4 * VP));
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, vop, o[db], 0, 0, 0);
-            }
+        for (int db = 0; db < ND; ++db) {
+            const half8 va = cat_half8(lds_read_tr16(vrd + 16 * db),
+                                       lds_read_tr16(vrd + 16 * VP + 16 * db));
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pt, o[db], 0, 0, 0);
         }
     };
 
@@ -323,79 +332,71 @@ decode_splitk_kernel(const DecodeArgs a) {
     using Pf = std::true_type;
     using NoPf = std::false_type;
     load_k(I0{}, t_begin);
-    load_v(I0{}, t_begin);
+    load_v(t_begin);
     load_k(I1{}, t_begin + TOK);
-    load_v(I1{}, t_begin + TOK);
     int it = 0;
     for (; it + 3 < n_iter; it += 2) {
-        step(I0{}, Pf{}, it);
-        step(I1{}, Pf{}, it + 1);
+        step(I0{}, Pf{}, Pf{}, it);
+        step(I1{}, Pf{}, Pf{}, it + 1);
     }
-    // tail: at most three iterations, no further prefetch past the split
+    // tail: at most three steps, no loads past the split
     if (it + 2 < n_iter) {
-        step(I0{}, Pf{}, it);
-        step(I1{}, NoPf{}, it + 1);
-        step(I0{}, NoPf{}, it + 2);
+        step(I0{}, Pf{}, Pf{}, it);
+        step(I1{}, NoPf{}, Pf{}, it + 1);
+        step(I0{}, NoPf{}, NoPf{}, it + 2);
+    } else if (it + 1 < n_iter) {
+        step(I0{}, NoPf{}, Pf{}, it);
+        step(I1{}, NoPf{}, NoPf{}, it + 1);
     } else {
-        step(I0{}, NoPf{}, it);
-        if (it + 1 < n_iter) step(I1{}, NoPf{}, it + 1);
+        step(I0{}, NoPf{}, NoPf{}, it);
     }
 
-    // ---- row sums over the lanes that share this lane's heads.
-    float l_tot[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        float x = row16_sum(l_part[e]);
-        if constexpr (R == 1) x += __shfl_xor(x, 16);
-        if constexpr (R <= 2) x += __shfl_xor(x, 32);
-        l_tot[e] = x;
-    }
-
-    // Lane (g, col) holds O[head 4*(g%R)+e][dim 16*db + col]; the REP lane
-    // groups with equal g%R hold identical rows and split the stores by db.
-    const int hg = g % R;
-    const int rep = g / R;
+    const float l_tot = rows4_sum(l_part);
+    if (!hvalid) return;
+    const int64_t qrow = row0 + col;
     if (nsb == 1) {
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        f16* orow = a.out + qrow * D + 4 * g;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int h = 4 * hg + e;
-            if (h >= G) continue;
-            const float inv = l_tot[e] > 0.f ? 1.f / l_tot[e] : 0.f;
-            f16* orow = a.out + (row0 + h) * D;
+        for (int db = 0; db < ND; ++db) {
+            half4 h;
 #pragma unroll
-            for (int db = 0; db < ND; ++db)
-                if (db % REP == rep) orow[16 * db + col] = static_cast<f16>(o[db][e] * inv);
+            for (int e = 0; e < 4; ++e) h[e] = static_cast<f16>(o[db][e] * inv);
+            *reinterpret_cast<half4*>(orow + 16 * db) = h;
         }
         return;
     }
+    const int64_t prow = qrow * a.nsplit + split;
+    float* po = a.ws_o + prow * D + 4 * g;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int h = 4 * hg + e;
-        if (h >= G) continue;
-        const int64_t prow = (row0 + h) * a.nsplit + split;
-        float* po = a.ws_o + prow * D;
-#pragma unroll
-        for (int db = 0; db < ND; ++db)
-            if (db % REP == rep) po[16 * db + col] = o[db][e];
-        if (col == 0 && rep == 0) {
-            a.ws_ml[prow * 2] = m_run[e];
-            a.ws_ml[prow * 2 + 1] = l_tot[e];
-        }
+    for (int db = 0; db < ND; ++db) *reinterpret_cast<floatx4*>(po + 16 * db) = o[db];
+    if (g == 0) {
+        a.ws_ml[prow * 2] = m_run * sc;  // log2 units
+        a.ws_ml[prow * 2 + 1] = l_tot;
     }
 }
 
-// Log-sum-exp merge of the split partials of one (kv_head, sequence): weights
-// first (lanes over splits, all heads' (m, l) loads in flight at once), then
-// lanes over (head, 8-dim group) accumulate the weighted partials.
+// Log-sum-exp merge of the split partials of one (kv_head, sequence), four
+// waves per workgroup: all threads stage (m, l) of every (head, split) in
+// LDS; wave w turns heads w, w+4, ... into merge weights; then wave w sums
+// splits w, w+4, ... of every (head, 8-dim group) with all its loads in
+// flight at once, and the four partial sums are added through LDS.
+constexpr int kMergeWaves = 4;
+
 template <int D, int G>
-__global__ void __launch_bounds__(kWave)
+__global__ void __launch_bounds__(kMergeWaves * kWave)
 decode_merge_kernel(const DecodeArgs a) {
-    constexpr int LPR = D / 8;
-    constexpr int HPP = kWave / LPR;  // heads per pass
+    constexpr int LPR = D / 8;          // lanes per head row (8 dims each)
+    constexpr int HPP = kWave / LPR;    // heads per pass of one wave
+    constexpr int NP = (G + HPP - 1) / HPP;
+    constexpr int U = 8;                // splits in flight per lane
     __shared__ float w_lds[G][kMaxSplits];
     __shared__ float l_lds[G][kMaxSplits];
+    __shared__ __attribute__((aligned(16))) float red[kMergeWaves - 1][NP * HPP][D];
 
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = blockIdx.x;
     const int b = blockIdx.y;
     const int64_t row0 = (int64_t)b * a.Hq + (int64_t)kvh * G;
@@ -405,24 +406,14 @@ decode_merge_kernel(const DecodeArgs a) {
     const int nsb = (L + a.chunk - 1) / a.chunk;
     if (nsb <= 1) return;  // written directly by the split kernel
 
-    for (int j0 = 0; j0 < nsb; j0 += kWave) {
-        const int j = j0 + lane;
-        float2 v[G];
-#pragma unroll
-        for (int h = 0; h < G; ++h)
-            v[h] = j < nsb ? *reinterpret_cast<const float2*>(a.ws_ml + ((row0 + h) * a.nsplit + j) * 2)
-                           : float2{-INFINITY, 0.f};
-        if (j < nsb) {
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                w_lds[h][j] = v[h].x;
-                l_lds[h][j] = v[h].y;
-            }
-        }
+    for (int i = tid; i < G * nsb; i += kMergeWaves * kWave) {
+        const int h = i / nsb, j = i - h * nsb;
+        const float2 v = *reinterpret_cast<const float2*>(a.ws_ml + ((row0 + h) * a.nsplit + j) * 2);
+        w_lds[h][j] = v.x;
+        l_lds[h][j] = v.y;
     }
     __syncthreads();
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
+    for (int h = wave; h < G; h += kMergeWaves) {
         float mx = -INFINITY;
         for (int j = lane; j < nsb; j += kWave) mx = fmaxf(mx, w_lds[h][j]);
         mx = wave_max(mx);
@@ -433,37 +424,54 @@ decode_merge_kernel(const DecodeArgs a) {
         for (int j = lane; j < nsb; j += kWave) w_lds[h][j] = fast_exp2(w_lds[h][j] - mx) * inv;
     }
     __syncthreads();
+
+    floatx4 acc[NP][2];
 #pragma unroll
-    for (int h0 = 0; h0 < G; h0 += HPP) {
-        const int h = h0 + lane / LPR;
+    for (int p = 0; p < NP; ++p) {
+        acc[p][0] = floatx4{0.f, 0.f, 0.f, 0.f};
+        acc[p][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+        const int h = p * HPP + lane / LPR;
         if (h >= G) continue;
         const float* po = a.ws_o + (row0 + h) * a.nsplit * D + 8 * (lane % LPR);
-        floatx4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-        int j = 0;
-        for (; j + 4 <= nsb; j += 4) {
-            floatx4 x[4][2];
+        for (int j0 = wave; j0 < nsb; j0 += kMergeWaves * U) {
+            floatx4 x[U][2];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                x[u][0] = *reinterpret_cast<const floatx4*>(po + (j + u) * D);
-                x[u][1] = *reinterpret_cast<const floatx4*>(po + (j + u) * D + 4);
+            for (int u = 0; u < U; ++u) {
+                const int j = min(j0 + kMergeWaves * u, nsb - 1);
+                x[u][0] = *reinterpret_cast<const floatx4*>(po + (int64_t)j * D);
+                x[u][1] = *reinterpret_cast<const floatx4*>(po + (int64_t)j * D + 4);
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float w = w_lds[h][j + u];
-                o0 += w * x[u][0];
-                o1 += w * x[u][1];
+            for (int u = 0; u < U; ++u) {
+                const int j = j0 + kMergeWaves * u;
+                const float w = j < nsb ? w_lds[h][j] : 0.f;
+                acc[p][0] += w * x[u][0];
+                acc[p][1] += w * x[u][1];
             }
         }
-        for (; j < nsb; ++j) {
-            const float w = w_lds[h][j];
-            o0 += w * *reinterpret_cast<const floatx4*>(po + j * D);
-            o1 += w * *reinterpret_cast<const floatx4*>(po + j * D + 4);
+        if (wave > 0) {
+            float* r = &red[wave - 1][p * HPP + lane / LPR][8 * (lane % LPR)];
+            *reinterpret_cast<floatx4*>(r) = acc[p][0];
+            *reinterpret_cast<floatx4*>(r + 4) = acc[p][1];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int h = p * HPP + lane / LPR;
+        if (h >= G) continue;
+#pragma unroll
+        for (int w = 0; w < kMergeWaves - 1; ++w) {
+            const float* r = &red[w][p * HPP + lane / LPR][8 * (lane % LPR)];
+            acc[p][0] += *reinterpret_cast<const floatx4*>(r);
+            acc[p][1] += *reinterpret_cast<const floatx4*>(r + 4);
         }
         half8 hv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            hv[e] = static_cast<f16>(o0[e]);
-            hv[4 + e] = static_cast<f16>(o1[e]);
+            hv[e] = static_cast<f16>(acc[p][0][e]);
+            hv[4 + e] = static_cast<f16>(acc[p][1][e]);
         }
         store_half8(a.out + (row0 + h) * D + 8 * (lane % LPR), hv);
     }
@@ -582,6 +590,16 @@ Plan make_plan(int batch, int num_kv_heads, int max_seq_len, int num_splits) {
 // exactly nsplit*B*Hq*(D+2) floats, the split_buffer size the reference's
 // callers allocate (forward_gpu.cu:100, test_attention.cpp:124).  Only the
 // fast kernels (D = 64 or 128) split, so the (m, l) block stays 16-B aligned.
+// A paged split covers at most kMaxPagedChunk tokens.
+Plan plan_for(int batch, int num_kv_heads, int max_seq_len, int num_splits, bool paged) {
+    Plan p = make_plan(batch, num_kv_heads, max_seq_len, num_splits);
+    if (paged && p.chunk > kMaxPagedChunk) {
+        p.chunk = kMaxPagedChunk;
+        p.nsplit = (max_seq_len + kMaxPagedChunk - 1) / kMaxPagedChunk;
+    }
+    return p;
+}
+
 size_t workspace_bytes_for(int batch, int hq, int hkv, int d, const Plan& p) {
     (void)hkv;
     if (p.nsplit <= 1) return 0;
@@ -630,7 +648,10 @@ KVDev to_dev(const kvhp_kv_view& v) {
 }
 
 bool view_fast_ok(const kvhp_kv_view& v) {
-    if (v.stride_d != 1 || v.stride_s % 8 != 0 || !aligned16(v.data)) return false;
+    // Rows are addressed with 32-bit byte offsets inside a 16-row page.
+    if (v.stride_d != 1 || v.stride_s % 8 != 0 || v.stride_s <= 0 || v.stride_s >= (1 << 26) ||
+        !aligned16(v.data))
+        return false;
     if (v.block_table) return v.page_size == kPage && v.stride_h % 8 == 0;
     return v.stride_b % 8 == 0 && v.stride_h % 8 == 0;
 }
@@ -643,7 +664,8 @@ void launch_fast(const DecodeArgs& a, dim3 grid, bool paged, hipStream_t s) {
     else
         hipLaunchKernelGGL((decode_splitk_kernel<D, G, false>), grid, dim3(kWave), 0, s, a);
     if (a.nsplit > 1)
-        hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.Hkv, grid.z), dim3(kWave), 0, s, a);
+        hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.Hkv, grid.z), dim3(kMergeWaves * kWave),
+                           0, s, a);
 }
 
 template <int D>
@@ -714,8 +736,10 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
     const bool shared_table = !paged || (kv->block_table == vv->block_table &&
                                          kv->max_pages == vv->max_pages &&
                                          kv->num_pages == vv->num_pages);
+    const Plan plan = plan_for(batch, hkv, max_seq_len, num_splits, paged);
     const bool fast = (d == 64 || d == 128) && fast_group(G) && view_fast_ok(*kv) &&
-                      view_fast_ok(*vv) && aligned16(q) && aligned16(out) && shared_table;
+                      view_fast_ok(*vv) && aligned16(q) && aligned16(out) && shared_table &&
+                      plan.nsplit <= kMaxSplits;
     if (!fast) {
         // Single pass: every sequence fully, no workspace.
         a.ws_o = nullptr;
@@ -733,7 +757,6 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
         return check_launch("decode_attention(generic)");
     }
 
-    const Plan plan = make_plan(batch, hkv, max_seq_len, num_splits);
     a.chunk = plan.chunk;
     a.nsplit = plan.nsplit;
     a.cap = plan.nsplit * plan.chunk;
@@ -780,8 +803,13 @@ extern "C" size_t kvhp_decode_workspace_bytes(int batch, int num_q_heads,
                                               int num_kv_heads, int head_dim,
                                               int max_seq_len, int num_splits) {
     if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
-    return workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim,
-                               make_plan(batch, num_kv_heads, max_seq_len, num_splits));
+    // the larger of the strided and the paged plan (a paged split is capped
+    // at kMaxPagedChunk tokens, which can mean more splits)
+    const size_t strided = workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim,
+                                               plan_for(batch, num_kv_heads, max_seq_len, num_splits, false));
+    const size_t paged = workspace_bytes_for(batch, num_q_heads, num_kv_heads, head_dim,
+                                             plan_for(batch, num_kv_heads, max_seq_len, num_splits, true));
+    return strided > paged ? strided : paged;
 }
 
 extern "C" int kvhp_decode_workspace_init(void* workspace, size_t workspace_bytes,

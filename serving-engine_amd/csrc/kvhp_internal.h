@@ -95,6 +95,11 @@ __device__ __forceinline__ half8 load_half8(const f16* p) {
     return *reinterpret_cast<const half8*>(p);
 }
 
+// Streaming read of data used once (KV cache rows): non-temporal hint.
+__device__ __forceinline__ half8 load_half8_stream(const f16* p) {
+    return __builtin_bit_cast(half8, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+}
+
 __device__ __forceinline__ void store_half8(f16* p, half8 v) {
     *reinterpret_cast<half8*>(p) = v;
 }

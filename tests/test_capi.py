@@ -97,7 +97,8 @@ def test_host_validation_errors():
                                    ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000), 1, 8, 4, 64,
                                    128, 0, None, 0, None)
     assert rc == kvhp.KVHP_ERR_INVALID and "paged" in kvhp.last_error()
-    # caller workspace too small for 16 splits
+    # caller workspace too small for 16 splits (a view the fast path takes)
+    v.stride_s, v.stride_h, v.stride_b = 64, 64 * 4096, 4 * 64 * 4096
     rc = lib.kvhp_decode_attention(ctypes.c_void_p(0x1000), ctypes.byref(v), ctypes.byref(v),
                                    ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000), 1, 8, 4, 64,
                                    4096, 16, ctypes.c_void_p(0x3000), 64, None)
