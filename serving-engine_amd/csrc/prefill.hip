@@ -45,6 +45,7 @@ namespace kvhp {
 namespace {
 
 constexpr int kBN = 64;     // keys per tile
+constexpr int kNumCUs = 256;  // MI355X compute units (work-split heuristic only)
 
 struct PrefillArgs {
     const f16* q;           // [B][S][Hq][D]
@@ -89,6 +90,14 @@ __device__ __forceinline__ void dma16(const f16* src, f16* lds_base) {
                  :: "s"(m0v), "v"(src) : "memory", "m0");
 }
 
+// Same with a wave-uniform base in SGPRs and a 32-bit per-lane byte offset.
+__device__ __forceinline__ void dma16s(const f16* sbase, uint32_t voff, f16* lds_base) {
+    const uint32_t m0v = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((lds_void*)(lds_f16*)lds_base));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :: "s"(m0v), "v"(voff), "s"(sbase) : "memory", "m0");
+}
+
 // s_waitcnt vmcnt(N) (expcnt / lgkmcnt left free).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -104,20 +113,51 @@ __device__ __forceinline__ void ring_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// A workgroup serves one KV head and a query block of 16*RB rows for all G
-// query heads of that KV head: G*RB "units" of (head, 16 rows), at most 8,
-// two per wave.  K/V tiles of 64 keys stream through a 4-stage LDS ring
-// filled by direct global->LDS loads; rows are stored XOR-swizzled (16-byte
-// chunk c of row r at position c ^ swz(r)) so the MFMA operand reads hit
-// distinct banks without padding.  Query blocks i and N-1-i run in the same
-// workgroup so every workgroup does the same causal work.
-template <int D, int WAVES>
-__global__ void __launch_bounds__(WAVES * kWave)
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLazyLog2 = 8.f;  // P stays below 2^8 between rescales
+
+// Sum / max across the two 32-lane halves of a wave (v_permlane32_swap).
+__device__ __forceinline__ float halves_max(float x) {
+    auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+
+// A workgroup of 8 waves serves one KV head and a query block of 32*RB rows
+// for all G query heads of that KV head: G*RB units of (head, 32 rows).  With
+// KG = 1 each wave owns one unit (G*RB <= 8); with KG = 2 (G <= 4) the waves
+// form two groups of four that share the units and split every 64-key tile
+// (group y takes keys 32y..32y+31), and the two softmax states of a unit are
+// merged through LDS at the end -- half the query rows per workgroup, so
+// twice the workgroups for short prompts.  K/V tiles of 64 keys stream through a 4-stage LDS ring
+// filled by direct global->LDS loads and are read by every wave, so GQA
+// heads share their K/V traffic; rows are stored XOR-swizzled (16-byte
+// chunk c of row r at position c ^ swz(r)) so the operand reads hit distinct
+// banks without padding.  Query blocks i and N-1-i run in the same workgroup
+// so every workgroup does the same causal work.
+//
+// Contractions on v_mfma_f32_32x32x16_f16 (lane l: row/column l%32, k-slots
+// 8(l/32)..+8; accumulator element i is row 8(i/4) + 4(l/32) + i%4):
+//   S^T = K Q^T     A = K rows (ds_read_b128), B = Q^T in registers; lane l
+//                   owns query row l%32 of its unit, 32 of the 64 keys.
+//   O^T += V^T P^T  per 16-key step t: A = V^T by two transposing 8-byte
+//                   reads, B = P^T = fp16 of accumulator elements 8u..8u+7
+//                   of key block t/2 (u = t%2): k-slot (h, e) is key
+//                   16t + 4h + e for e < 4 and 16t + 8 + 4h + e - 4 above.
+// Per 64-key tile a wave does 32 MFMAs (1 MFLOP) for 32 KB of LDS reads,
+// twice the work per LDS byte of 16x16 tiles.
+template <int D, int KG>
+__global__ void __launch_bounds__(8 * kWave)
 prefill_mfma_kernel(const PrefillArgs a) {
+    constexpr int WAVES = 8;
+    constexpr int UPG = WAVES / KG;     // units per wave group
     constexpr int NTH = WAVES * kWave;  // threads per workgroup
-    constexpr int NB = 8 / WAVES;       // units per wave (8 units per workgroup)
-    constexpr int NC = D / 32;          // k-chunks of the QK contraction
-    constexpr int ND = D / 16;          // 16-dim blocks of the output
+    constexpr int NC = D / 16;          // k-chunks of the QK contraction
+    constexpr int NDB = D / 32;         // 32-dim blocks of the output
     constexpr int CPR = D / 8;          // 16-byte chunks per row
     constexpr int RPI = kWave / CPR;    // rows per DMA instruction
     constexpr int IPW = kBN / RPI / WAVES;  // DMA instructions per wave per matrix
@@ -126,16 +166,16 @@ prefill_mfma_kernel(const PrefillArgs a) {
     constexpr int KSW = CPR - 1;        // K swizzle: c ^ (r & KSW)
     constexpr int VSW = CPR / 2 - 1;    // V swizzle: c ^ ((r & VSW) << 1)
 
-    __shared__ __attribute__((aligned(16))) f16 st0[2 * TB];
-    __shared__ __attribute__((aligned(16))) f16 st1[2 * TB];
-    __shared__ __attribute__((aligned(16))) f16 st2[2 * TB];
-    __shared__ __attribute__((aligned(16))) f16 st3[2 * TB];
+    constexpr int NSTAGE = 4;
+    __shared__ __attribute__((aligned(16))) f16 ring[NSTAGE * 2 * TB];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases in SGPRs
     const int lane = tid & 63;
-    const int g = lane >> 4;
-    const int col = lane & 15;
+    const int h = lane >> 5;        // k-slot half
+    const int c32 = lane & 31;      // row / column in the 32x32 operands
+    const int j16 = lane & 15;      // lane within its 16-lane block
+    const int blk2 = (lane >> 4) & 1;
 
     const int kvh = blockIdx.x % a.Hkv;
     const int pair = blockIdx.x / a.Hkv;
@@ -143,7 +183,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
     const int S = a.S;
     const int G = a.G;
     const int RB = a.RB;
-    const int BM = 16 * RB;
+    const int BM = 32 * RB;
     const int nunits = G * RB;
     const int64_t qrs = (int64_t)a.Hq * D;     // q/out row stride
     const int64_t kvrs = (int64_t)a.Hkv * D;   // k/v row stride
@@ -153,53 +193,88 @@ prefill_mfma_kernel(const PrefillArgs a) {
     // DMA of tile tt into a stage: this wave's rows (wave*IPW + p)*RPI + lane/CPR.
     // Tiles past the last one re-load the last tile (an L2 hit): every path
     // issues the same loads, so the vmcnt bookkeeping stays exact.
+    // Per-lane DMA source offsets inside a tile (bytes): row and swizzled chunk.
+    uint32_t dko[IPW], dvo[IPW];
+#pragma unroll
+    for (int p = 0; p < IPW; ++p) {
+        const int row = (wave * IPW + p) * RPI + lane / CPR;
+        const int ck = (lane % CPR) ^ (row & KSW);
+        const int cv = (lane % CPR) ^ ((row & VSW) << 1);
+        dko[p] = static_cast<uint32_t>((row * kvrs + 8 * ck) * 2);
+        dvo[p] = static_cast<uint32_t>((row * kvrs + 8 * cv) * 2);
+    }
     int last_tile = 0;
     auto issue = [&](f16* stg, int tt) {
         tt = min(tt, last_tile);
+        const int key0 = tt * kBN;
+        if (key0 + kBN <= S) {
+            const f16* kt = kb + (int64_t)key0 * kvrs;
+            const f16* vt = vb + (int64_t)key0 * kvrs;
 #pragma unroll
-        for (int p = 0; p < IPW; ++p) {
-            const int blk = wave * IPW + p;
-            const int row = blk * RPI + lane / CPR;
-            const int key = min(tt * kBN + row, S - 1);
-            const int ck = (lane % CPR) ^ (row & KSW);
-            const int cv = (lane % CPR) ^ ((row & VSW) << 1);
-            dma16(kb + (int64_t)key * kvrs + 8 * ck, stg + blk * RPI * D);
-            dma16(vb + (int64_t)key * kvrs + 8 * cv, stg + TB + blk * RPI * D);
+            for (int p = 0; p < IPW; ++p) {
+                const int blk = wave * IPW + p;
+                dma16s(kt, dko[p], stg + blk * RPI * D);
+                dma16s(vt, dvo[p], stg + TB + blk * RPI * D);
+            }
+        } else {
+            // the last, partial tile: rows past the prompt re-read row S-1
+#pragma unroll
+            for (int p = 0; p < IPW; ++p) {
+                const int blk = wave * IPW + p;
+                const int row = blk * RPI + lane / CPR;
+                const int key = min(key0 + row, S - 1);
+                const int ck = (lane % CPR) ^ (row & KSW);
+                const int cv = (lane % CPR) ^ ((row & VSW) << 1);
+                dma16(kb + (int64_t)key * kvrs + 8 * ck, stg + blk * RPI * D);
+                dma16(vb + (int64_t)key * kvrs + 8 * cv, stg + TB + blk * RPI * D);
+            }
         }
     };
+    // Per-lane LDS read offsets (halfs) inside a stage: K operand chunk c of
+    // key row 32*kgrp + c32 (+32 per extra key block), and V^T operand of dim
+    // block db at key row 32*kgrp + 4h + j16/4 (+16 per key step, +8 for the
+    // second read).  The swizzles depend on the lane only.
+    const int kgrp_ = wave / (WAVES / KG);
+    int kro[NC], vro[NDB];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int r = 32 * kgrp_ + c32;
+        kro[c] = r * D + 8 * ((2 * c + h) ^ (r & KSW));
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+        const int R1 = 32 * kgrp_ + 4 * h + j16 / 4;
+        const int ch = 4 * db + 2 * blk2 + ((j16 & 3) >> 1);
+        vro[db] = R1 * D + 8 * (ch ^ ((R1 & VSW) << 1)) + 4 * (j16 & 1);
+    }
 
     for (int pass = 0; pass < 2; ++pass) {
         const int qblk = pass == 0 ? pair : a.n_qblk - 1 - pair;
         if (pass == 1 && qblk <= pair) break;   // odd count: middle block once
         const int q0 = qblk * BM;
 
-        // ---- this wave's units: u = wave + WAVES*i -> head kvh*G + u%G, rows r0..r0+15
-        int r0[NB], qh[NB];
-        bool uvalid[NB];
-        half8 qop[NB][NC];
+        // ---- this wave's unit: head kvh*G + u%G, rows r0 .. r0+31; its key
+        //      half of every tile (all 64 keys when KG == 1)
+        const int u = wave % UPG;
+        const int kgrp = wave / UPG;
+        const bool uvalid = u < nunits;
+        const int qh = kvh * G + (uvalid ? u % G : 0);
+        const int r0 = q0 + 32 * (uvalid ? u / G : 0);
+        const int row = r0 + c32;
+        half8 qop[NC];
+        {
+            const bool live = uvalid && row < S;
+            const f16* qp = a.q + ((int64_t)b * S + row) * qrs + (int64_t)qh * D + 8 * h;
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const int u = wave + WAVES * i;
-            uvalid[i] = u < nunits;
-            qh[i] = kvh * G + (uvalid[i] ? u % G : 0);
-            r0[i] = q0 + 16 * (uvalid[i] ? u / G : 0);
-            const int row = r0[i] + col;
-            const bool live = uvalid[i] && row < S;
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-                qop[i][c] = live ? load_half8(a.q + ((int64_t)b * S + row) * qrs +
-                                              (int64_t)qh[i] * D + 32 * c + 8 * g)
-                                 : half8{};
+            for (int c = 0; c < NC; ++c) qop[c] = live ? load_half8(qp + 16 * c) : half8{};
         }
-        floatx4 o[NB][ND];
-        float m_run[NB], l_part[NB];
+        floatx16 o[NDB];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            m_run[i] = -1e30f;
-            l_part[i] = 0.f;
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int db = 0; db < ND; ++db) o[i][db] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
+            for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+        float m_run = -1e30f, l_part = 0.f;
+        const float lazy_thr = kLazyLog2 / a.scale_log2;   // in raw score units
 
         const int last_row = min(q0 + BM, S) - 1;
         const int n_tiles = last_row / kBN + 1;
@@ -207,144 +282,164 @@ prefill_mfma_kernel(const PrefillArgs a) {
 
         wait_vmcnt<0>();  // q in registers before the ring: no compiler waits inside it
         ring_barrier();   // everyone is done with the previous pass's stages
-        issue(st0, 0);
-        issue(st1, 1);
-        issue(st2, 2);
+        issue(ring, 0);
+        issue(ring + 2 * TB, 1);
+        issue(ring + 4 * TB, 2);
 
-        // One tile on stage STG: wait for this wave's DMA of the tile (the two
-        // later tiles stay in flight), barrier (all waves' DMA landed, the
-        // previous stage is free), refill the previous stage with tile kt+3,
-        // compute.
-        auto step = [&](f16* stg, f16* next_stg, int kt) {
-            wait_vmcnt<2 * LPT>();
-            ring_barrier();
-            issue(next_stg, kt + 3);
-
-            const int k0 = kt * kBN;
-            const f16* Kt = stg;
-            const f16* Vt = stg + TB;
-
-            // ---- S^T = K Q^T for both units, K operand shared.
-            bool act[NB];
+        // Software pipeline: step kt computes S^T of tile kt+1 (MFMA) before
+        // the softmax of tile kt (VALU), so the matrix cores work while the
+        // exponentials run, then O^T += V^T P^T for tile kt.  Step kt needs
+        // K of tile kt+1 and V of tile kt: wait for this wave's DMA of tile
+        // kt+1 (tile kt+2 stays in flight), barrier (all waves' DMA landed,
+        // the stage of tile kt-1 is free), refill that stage with tile kt+3.
+        constexpr int NKB = 2 / KG;     // this wave's 32-key blocks per tile
+        auto qk = [&](const f16* Kt, floatx16 (&sc)[NKB]) {
 #pragma unroll
-            for (int i = 0; i < NB; ++i) act[i] = uvalid[i] && k0 <= r0[i] + 15;
-            floatx4 sc[NB][4];
+            for (int kb2 = 0; kb2 < NKB; ++kb2) {
 #pragma unroll
-            for (int i = 0; i < NB; ++i)
-#pragma unroll
-                for (int kb4 = 0; kb4 < 4; ++kb4) sc[i][kb4] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kb4 = 0; kb4 < 4; ++kb4) {
-                const int r = 16 * kb4 + col;
+                for (int i = 0; i < 16; ++i) sc[kb2][i] = 0.f;
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
-                    const int pos = (4 * c + g) ^ (r & KSW);
-                    const half8 kop = *reinterpret_cast<const half8*>(&Kt[r * D + 8 * pos]);
-#pragma unroll
-                    for (int i = 0; i < NB; ++i)
-                        sc[i][kb4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[i][c],
-                                                                            sc[i][kb4], 0, 0, 0);
-                }
-            }
-
-            // ---- online softmax per unit; P^T operands straight from S^T.
-            // Inactive units (invalid, or entirely above the diagonal) see
-            // only -inf scores: alpha = 1 and p = 0 leave their state as is,
-            // so every MFMA above and below runs unconditionally (no
-            // branches, no conservative waits inside the ring).  The running
-            // max is kept on raw scores (scale > 0), and the scale is folded
-            // into the exp2 argument: p = 2^(s*c - m*c).
-            half8 pop[NB][2];
-#pragma unroll
-            for (int i = 0; i < NB; ++i) {
-                const int row = r0[i] + col;
-                const bool diag = !act[i] || k0 + kBN - 1 > r0[i];
-                if (diag) {
-#pragma unroll
-                    for (int kb4 = 0; kb4 < 4; ++kb4) {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int key = k0 + 16 * kb4 + 4 * g + e;
-                            if (!act[i] || key > row || key >= S) sc[i][kb4][e] = -INFINITY;
-                        }
-                    }
-                }
-                float tmax = -INFINITY;
-#pragma unroll
-                for (int kb4 = 0; kb4 < 4; ++kb4)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, sc[i][kb4][e]);
-                tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-                tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-                const float mn = fmaxf(m_run[i], tmax);
-                const float nmc = -mn * a.scale_log2;
-                float ls = 0.f;
-#pragma unroll
-                for (int kb4 = 0; kb4 < 4; ++kb4) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float p = fast_exp2(fmaf(sc[i][kb4][e], a.scale_log2, nmc));
-                        pop[i][kb4 / 2][(kb4 % 2) * 4 + e] = static_cast<f16>(p);
-                        ls += p;
-                    }
-                }
-                // Rescale only when some row's max moved (rare after the first
-                // tiles): a wave-uniform branch.
-                if (__builtin_amdgcn_read_exec() & __ballot(mn != m_run[i])) {
-                    const float alpha = fast_exp2((m_run[i] - mn) * a.scale_log2);
-                    l_part[i] *= alpha;
-#pragma unroll
-                    for (int db = 0; db < ND; ++db) o[i][db] *= alpha;
-                }
-                m_run[i] = mn;
-                l_part[i] += ls;
-            }
-
-            // ---- O^T += V^T P^T; k-slot (g,e') of step ks is key
-            //      ks*32 + (e' < 4 ? 4g + e' : 16 + 4g + e' - 4).
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int R1 = 32 * ks + 4 * g + col / 4;
-                const int R2 = R1 + 16;
-                const int h = 4 * ((col % 4) & 1);
-#pragma unroll
-                for (int db = 0; db < ND; ++db) {
-                    const int c = 2 * db + ((col % 4) >> 1);
-                    const f16* p1 = &Vt[R1 * D + 8 * (c ^ ((R1 & VSW) << 1)) + h];
-                    const f16* p2 = &Vt[R2 * D + 8 * (c ^ ((R2 & VSW) << 1)) + h];
-                    const half8 vop = cat_half8(lds_read_tr16(p1), lds_read_tr16(p2));
-#pragma unroll
-                    for (int i = 0; i < NB; ++i)
-                        o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[i][ks],
-                                                                          o[i][db], 0, 0, 0);
+                    const half8 kop = *reinterpret_cast<const half8*>(&Kt[kro[c] + 32 * kb2 * D]);
+                    sc[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[c], sc[kb2], 0, 0, 0);
                 }
             }
         };
 
-        for (int kt = 0; kt < n_tiles; kt += 4) {
-            step(st0, st3, kt);
-            if (kt + 1 < n_tiles) step(st1, st0, kt + 1);
-            if (kt + 2 < n_tiles) step(st2, st1, kt + 2);
-            if (kt + 3 < n_tiles) step(st3, st2, kt + 3);
+        floatx16 scur[NKB], snext[NKB];
+        wait_vmcnt<2 * LPT>();
+        ring_barrier();
+        qk(ring, scur);
+
+        for (int kt = 0; kt < n_tiles; ++kt) {
+            const f16* cur = ring + (kt % NSTAGE) * 2 * TB;
+            wait_vmcnt<LPT>();
+            ring_barrier();
+            issue(ring + ((kt + NSTAGE - 1) % NSTAGE) * 2 * TB, kt + 3);
+            // tile kt+1 (the last tile again past the end: its result unused)
+            qk(ring + ((kt + 1) % NSTAGE) * 2 * TB, snext);
+
+            const int k0 = kt * kBN;
+            const bool act = uvalid && k0 <= r0 + 31;
+            // ---- online softmax of query row `row`; P^T operands straight
+            // from S^T.  Inactive units (invalid, or entirely above the
+            // diagonal) see only -inf scores: alpha = 1 and p = 0 leave their
+            // state as is, so every MFMA runs unconditionally (no branches,
+            // no conservative waits inside the ring).  The running max is
+            // kept on raw scores and the scale folded into the exponent.
+            if (!act || k0 + kBN - 1 > r0) {
+#pragma unroll
+                for (int kb2 = 0; kb2 < NKB; ++kb2)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = k0 + 32 * (kb2 + kgrp) + 8 * (i / 4) + 4 * h + (i % 4);
+                        if (!act || key > row || key >= S) scur[kb2][i] = -INFINITY;
+                    }
+            }
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int kb2 = 0; kb2 < NKB; ++kb2)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, scur[kb2][i]);
+            tmax = halves_max(tmax);
+            // Lazy rescale: m_run is a reference max, moved (and O, l
+            // rescaled) only when some row's max exceeds it by more than
+            // kLazyLog2 in log2 units; otherwise p = 2^(s*c - m_run*c) stays
+            // below 2^kLazyLog2, exact in fp16.  A wave-uniform branch taken
+            // on the first tiles and rarely after.
+            if (__builtin_amdgcn_read_exec() & __ballot(tmax > m_run + lazy_thr)) {
+                const float mn = fmaxf(m_run, tmax);
+                const float alpha = fast_exp2((m_run - mn) * a.scale_log2);
+                l_part *= alpha;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+                m_run = mn;
+            }
+            const float nmc = -m_run * a.scale_log2;
+            half8 pop[2 * NKB];
+            float ls = 0.f;
+#pragma unroll
+            for (int t = 0; t < 2 * NKB; ++t)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float p = fast_exp2(fmaf(scur[t / 2][8 * (t % 2) + e], a.scale_log2, nmc));
+                    pop[t][e] = static_cast<f16>(p);
+                    ls += p;
+                }
+            l_part += ls;
+
+            // ---- O^T += V^T P^T: lane j16 of 16-lane block (h, blk2) reads
+            //      rows R(j16/4) at dims 32db + 16*blk2 + 4*(j16%4).
+            const f16* Vt = cur + TB;
+#pragma unroll
+            for (int t = 0; t < 2 * NKB; ++t) {
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const f16* p1 = &Vt[vro[db] + 16 * t * D];
+                    const half8 vop = cat_half8(lds_read_tr16(p1), lds_read_tr16(p1 + 8 * D));
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pop[t], o[db], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int kb2 = 0; kb2 < NKB; ++kb2) scur[kb2] = snext[kb2];
         }
         wait_vmcnt<0>();  // drain the ring's trailing re-loads
 
-        // ---- normalise and store: lane holds row r0+col, dims 16db + 4g + e.
+        if constexpr (KG == 2) {
+            // ---- group 1 hands its (m, l, O) to group 0 through the ring's
+            //      LDS (every wave is past its last read of the ring).
+            float* xo = reinterpret_cast<float*>(ring);
+            float* xml = xo + UPG * NDB * 16 * kWave;
+            ring_barrier();
+            if (kgrp == 1) {
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            float lt = l_part[i];
-            lt += __shfl_xor(lt, 16);
-            lt += __shfl_xor(lt, 32);
-            const int row = r0[i] + col;
-            if (!uvalid[i] || row >= S) continue;
-            const float inv = lt > 0.f ? 1.f / lt : 0.f;
-            f16* orow = a.out + ((int64_t)b * S + row) * qrs + (int64_t)qh[i] * D;
+                for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int db = 0; db < ND; ++db) {
-                half4 hv;
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        floatx4 v4 = {o[db][4 * q4], o[db][4 * q4 + 1], o[db][4 * q4 + 2],
+                                      o[db][4 * q4 + 3]};
+                        *reinterpret_cast<floatx4*>(
+                            &xo[(((u * NDB + db) * 4 + q4) * kWave + lane) * 4]) = v4;
+                    }
+                xml[(u * kWave + lane) * 2] = m_run;
+                xml[(u * kWave + lane) * 2 + 1] = l_part;
+            }
+            ring_barrier();
+            if (kgrp == 0) {
+                const float m1 = xml[(u * kWave + lane) * 2];
+                const float l1 = xml[(u * kWave + lane) * 2 + 1];
+                const float mn = fmaxf(m_run, m1);
+                const float a0 = fast_exp2((m_run - mn) * a.scale_log2);
+                const float a1 = fast_exp2((m1 - mn) * a.scale_log2);
+                l_part = l_part * a0 + l1 * a1;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) hv[e] = static_cast<f16>(o[i][db][e] * inv);
-                *reinterpret_cast<half4*>(orow + 16 * db + 4 * g) = hv;
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        const floatx4 v4 = *reinterpret_cast<const floatx4*>(
+                            &xo[(((u * NDB + db) * 4 + q4) * kWave + lane) * 4]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            o[db][4 * q4 + e] = o[db][4 * q4 + e] * a0 + v4[e] * a1;
+                    }
+            }
+        }
+
+        // ---- normalise and store: lane holds row `row`, dims 32db + 8q + 4h + e.
+        {
+            const float lt = halves_sum(l_part);
+            if (kgrp == 0 && uvalid && row < S) {
+                const float inv = lt > 0.f ? 1.f / lt : 0.f;
+                f16* orow = a.out + ((int64_t)b * S + row) * qrs + (int64_t)qh * D + 4 * h;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        half4 hv;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) hv[e] = static_cast<f16>(o[db][4 * q4 + e] * inv);
+                        *reinterpret_cast<half4*>(orow + 32 * db + 8 * q4) = hv;
+                    }
             }
         }
 
@@ -472,16 +567,27 @@ int prefill_impl(const void* q, const void* k, const void* v, void* out, int64_t
                       aligned16(v) && aligned16(out) &&
                       (!pool_k || (aligned16(pool_k) && aligned16(pool_v)));
     if (fast) {
-        // units of (head, 16 rows) per workgroup: G*RB <= 8, two per wave
-        a.RB = 8 / a.G;
-        const int bm = 16 * a.RB;
+        // units of (head, 32 rows) per workgroup: one per wave, or (G <= 4)
+        // one per pair of waves that split each tile's keys
+        // Split each tile's keys across two wave groups (twice the
+        // workgroups) only when one unit per wave would leave fewer than two
+        // workgroups per CU: the split halves the work per barrier.
+        const int64_t qblk1 = (seq_len + 32 * (8 / a.G) - 1) / (32 * (8 / a.G));
+        const int64_t grid1 = (int64_t)hkv * ((qblk1 + 1) / 2) * batch;
+        const int kg = ((a.G == 1 || a.G == 2 || a.G == 4) && grid1 < 2 * kNumCUs) ? 2 : 1;
+        a.RB = 8 / kg / a.G;
+        const int bm = 32 * a.RB;
         a.n_qblk = static_cast<int>((seq_len + bm - 1) / bm);
         dim3 grid(hkv * ((a.n_qblk + 1) / 2), batch);
-        constexpr int W = 8;  // waves per workgroup: one 16-row unit each
-        if (d == 64)
-            hipLaunchKernelGGL((prefill_mfma_kernel<64, W>), grid, dim3(W * kWave), 0, s, a);
+        const dim3 blk(8 * kWave);
+        if (d == 64 && kg == 2)
+            hipLaunchKernelGGL((prefill_mfma_kernel<64, 2>), grid, blk, 0, s, a);
+        else if (d == 64)
+            hipLaunchKernelGGL((prefill_mfma_kernel<64, 1>), grid, blk, 0, s, a);
+        else if (kg == 2)
+            hipLaunchKernelGGL((prefill_mfma_kernel<128, 2>), grid, blk, 0, s, a);
         else
-            hipLaunchKernelGGL((prefill_mfma_kernel<128, W>), grid, dim3(W * kWave), 0, s, a);
+            hipLaunchKernelGGL((prefill_mfma_kernel<128, 1>), grid, blk, 0, s, a);
         return check_launch("flash_prefill");
     }
     dim3 grid(hq, static_cast<unsigned>(seq_len), batch);
