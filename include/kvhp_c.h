@@ -163,6 +163,74 @@ int kvhp_causal_gqa(const void* q, const void* k, const void* v, void* out,
                     int64_t seq_len, int64_t num_q_heads, int64_t num_kv_heads,
                     int64_t head_dim, void* stream);
 
+/* ---- Model operators around the KV-cache path (decoder-only model,
+ * batch-1 decode).  fp16 tensors row-major; W [N][K] is the PyTorch linear
+ * weight layout the reference uses (src/cuda/kernels.h:178-192). ---------- */
+
+/* Replaces engine::cuda::gemv (src/cuda/kernels.h:207-217,
+ * src/cuda/gemv.cu:29-63): y[n] = sum_k W[n][k] x[k], fp32 accumulation,
+ * fp16 y. */
+int kvhp_gemv(const void* W, const void* x, void* y, int N, int K, void* stream);
+/* Replaces engine::cuda::gemv_residual (src/cuda/kernels.h:231-241):
+ * y[n] = dot(W[n], x) + r[n]; r may alias y (in-place residual stream). */
+int kvhp_gemv_residual(const void* W, const void* x, const void* r, void* y, int N, int K,
+                       void* stream);
+/* rmsnorm (src/cuda/kernels.h:24-32) fused into the following GEMV:
+ * xn = fp16(x * rsqrt(mean(x^2) + eps) * norm_w), y = W xn, written to
+ * exactly one of y16 (fp16) or y32 (fp32, the reference's fp32 logits,
+ * kernels.h:194-205). */
+int kvhp_rmsnorm_gemv(const void* W, const void* x, const void* norm_w, float eps, void* y16,
+                      float* y32, int N, int K, void* stream);
+/* rmsnorm + gate/up projections + swiglu (kernels.h:150-158) in one pass:
+ * W_gate_up = [gate; up], [2N][K]; out[n] = silu(g) * u with g, u the fp16
+ * projections of the normalised x. */
+int kvhp_rmsnorm_gemv_swiglu(const void* W_gate_up, const void* x, const void* norm_w, float eps,
+                             void* out, int N, int K, void* stream);
+/* rmsnorm + fused q/k/v projection + apply_rope (kernels.h:57-70) +
+ * append_kv_cache (src/runtime/kv_cache.h:80-91) for one decode token:
+ * W_qkv = [Wq; Wk; Wv], [(Hq + 2 Hkv) D][K]; the token sits at position
+ * seq_len[0] - 1 (device int32: "bump, then write at num_tokens - 1");
+ * q_out [Hq][D] gets rotated q, rotated k and v go into page
+ * block_table[pos/16] slot pos%16 of pools [Hkv][num_pages][16][D]. */
+int kvhp_rmsnorm_qkv_rope_append(const void* W_qkv, const void* x, const void* norm_w, float eps,
+                                 const int32_t* seq_len, float rope_theta, void* q_out,
+                                 void* pool_k, void* pool_v, const int32_t* block_table,
+                                 int max_pages, int num_pages, int num_q_heads, int num_kv_heads,
+                                 int head_dim, int K, void* stream);
+/* Replaces engine::cuda::rmsnorm (kernels.h:24-32): rows x dim, fp32 math. */
+int kvhp_rmsnorm(const void* x, const void* weight, void* out, int64_t rows, int64_t dim,
+                 float eps, void* stream);
+/* Replaces engine::cuda::apply_rope (kernels.h:57-70): half-split RoPE in
+ * place on q [S][Hq][D], k [S][Hkv][D], positions start_pos.. */
+int kvhp_apply_rope(void* q, void* k, int64_t seq_len, int64_t num_q_heads, int64_t num_kv_heads,
+                    int64_t head_dim, int64_t start_pos, float rope_theta, void* stream);
+/* Prefill helper: split a fused projection [S][(Hq + 2 Hkv) D] into
+ * contiguous q [S][Hq][D], k, v [S][Hkv][D], with RoPE on q and k. */
+int kvhp_split_qkv_rope(const void* qkv, int64_t seq_len, int num_q_heads, int num_kv_heads,
+                        int head_dim, int64_t start_pos, float rope_theta, void* q, void* k,
+                        void* v, void* stream);
+/* Replaces engine::cuda::swiglu (kernels.h:150-158): out = silu(g) * u. */
+int kvhp_swiglu(const void* gate, const void* up, void* out, int64_t count, void* stream);
+/* swiglu over rows of a fused [gate | up] buffer [rows][2n] -> out [rows][n]. */
+int kvhp_swiglu_rows(const void* gate_up, void* out, int64_t rows, int64_t n, void* stream);
+/* Replaces engine::cuda::embedding_lookup (kernels.h:12-20) with device
+ * int32 ids (ids outside [0, vocab) give zero rows). */
+int kvhp_embedding(const int32_t* token_ids, const void* table, void* out, int64_t n,
+                   int64_t hidden, int64_t vocab, void* stream);
+/* Greedy sampling on device (the reference's host argmax loop,
+ * apps/generate.cpp:714-721): token = argmax of fp32 logits, lowest index
+ * on ties, NaN never chosen.  Optional: log[*log_count] = token and
+ * ++*log_count; ++*seq_len (the next step's "bump"). */
+int kvhp_argmax(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, int32_t* log,
+                int32_t* log_count, void* stream);
+/* Seeded N(0, std_dev) fp16 fill (synthetic weights): element i of stream
+ * stream_id is a Box-Muller normal of two splitmix64 hashes of
+ * (seed, stream_id, i). */
+int kvhp_randn_f16(void* out, int64_t count, uint64_t seed, uint64_t stream_id, float std_dev,
+                   void* stream);
+/* Constant fp16 fill. */
+int kvhp_fill_f16(void* out, int64_t count, float value, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -91,21 +91,6 @@ __device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
     return __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// Max / sum across the four 16-lane rows of a wave with the gfx950 row
-// swaps (VALU only, no LDS round trip).  Rows 0<->1, 2<->3, then 01<->23.
-__device__ __forceinline__ float rows4_max(float x) {
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
-}
-__device__ __forceinline__ float rows4_sum(float x) {
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
-}
-
 // One 64-lane workgroup per (split, kv_head, sequence).  Both contractions
 // are transposed so that lane (g, col) -- g = lane/16, col = lane%16 -- owns
 // query head `col` of the KV head's group for the whole online softmax:

@@ -91,6 +91,24 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// Max / sum across the four 16-lane rows of a wave with the gfx950 row
+// swaps (VALU only, no LDS round trip): rows 0<->1 and 2<->3, then 01<->23.
+__device__ __forceinline__ float rows4_max(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+// Full-wave sum without LDS: DPP within each 16-lane row, then row swaps.
+__device__ __forceinline__ float wave_sum_fast(float x) { return rows4_sum(row16_sum(x)); }
+__device__ __forceinline__ float wave_max_fast(float x) { return rows4_max(row16_max(x)); }
+
 __device__ __forceinline__ half8 load_half8(const f16* p) {
     return *reinterpret_cast<const half8*>(p);
 }

@@ -1,0 +1,730 @@
+// model_ops.hip -- operators of the decoder-only model around the KV-cache
+// path (config 5: Llama-style 1.1B, batch-1 greedy decode), for gfx950.
+//
+// Decode (one token) is HBM-bound on the weights: every projection is a
+// GEMV y = W x with W fp16 [N][K] row-major, read once.  A wave owns RW
+// output rows; lane l holds the 16-byte chunks 512j + 8l .. +8 of x in
+// registers for the whole kernel and streams the same chunks of its rows
+// (RW*K/512 non-temporal 16-byte loads in flight per lane), multiplies with
+// v_dot2_f32_f16 (fp16 products, fp32 accumulation) and reduces each row
+// across the wave with DPP + row swaps.  The neighbouring element-wise work
+// of the reference's decode step is fused into that kernel:
+//   prologue  RMSNorm of x (sum of squares in fp32, x*rsqrt*w rounded to
+//             fp16 as the reference's norm_out buffer, rmsnorm.cu:16-70);
+//   epilogue  fp16 store, residual add (gemv_residual, gemv.cu), fp32 logits,
+//             SwiGLU of a gate row and its up row (swiglu.cu; the gate and up
+//             values are rounded to fp16 first, as the reference's separate
+//             GEMV outputs are), or RoPE + KV-cache append for the fused QKV
+//             projection (rope.cu:8-57 then kv_cache.cu:8-36: q/k rounded to
+//             fp16, rotated in fp32, rounded again; k and v written into their
+//             16-token pages at position seq_len - 1).
+// A generic one-wave-per-row kernel covers shapes the fast one does not.
+//
+// Prefill uses library GEMMs (rocBLAS) for the projections; the row-wise
+// RMSNorm, the RoPE that also splits the fused QKV output, and SwiGLU over
+// the fused gate|up output are here.  Greedy sampling is an on-device argmax
+// with the lowest index winning ties (the reference's host loop,
+// generate.cpp:714-721), which also advances the device-side sequence length
+// so that a captured decode step needs no host round trip.
+#include "kvhp_internal.h"
+
+#include <cmath>
+
+namespace kvhp {
+
+namespace {
+
+typedef f16 half2v __attribute__((ext_vector_type(2)));
+
+enum Epilogue : int { kEpiF16 = 0, kEpiResidual = 1, kEpiF32 = 2, kEpiSwiglu = 3, kEpiQKV = 4 };
+
+struct GemvArgs {
+    const f16* W;          // [rows][K]
+    const f16* x;          // [K]
+    const f16* norm_w;     // [K] RMSNorm weight (prologue), or null
+    float eps;
+    int N;                 // output rows (SwiGLU: gate rows, up rows follow)
+    int K;
+    f16* y16;              // fp16 output
+    float* y32;            // fp32 output
+    const f16* resid;      // residual added in the epilogue (may alias y16)
+    // fused QKV: rows [Hq*D q | Hkv*D k | Hkv*D v]
+    int Hq, Hkv, D;
+    const int32_t* seq_len;  // device: the token is at position seq_len[0] - 1
+    float theta;
+    f16* pool_k;           // [Hkv][num_pages][16][D]
+    f16* pool_v;
+    const int32_t* bt;     // block table of the sequence [max_pages]
+    int max_pages, num_pages;
+};
+
+__device__ __forceinline__ float dot8(half8 a, half8 b, float acc) {
+    acc = __builtin_amdgcn_fdot2(half2v{a[0], a[1]}, half2v{b[0], b[1]}, acc, false);
+    acc = __builtin_amdgcn_fdot2(half2v{a[2], a[3]}, half2v{b[2], b[3]}, acc, false);
+    acc = __builtin_amdgcn_fdot2(half2v{a[4], a[5]}, half2v{b[4], b[5]}, acc, false);
+    acc = __builtin_amdgcn_fdot2(half2v{a[6], a[7]}, half2v{b[6], b[7]}, acc, false);
+    return acc;
+}
+
+__device__ __forceinline__ float round16(float v) { return static_cast<float>(static_cast<f16>(v)); }
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
+
+// RoPE angle of dimension pair i (< D/2) at position pos, as the reference
+// computes it in float (ops.cpp:174-186).
+__device__ __forceinline__ void rope_cs(int pos, int i, int D, float theta, float& c, float& s) {
+    const float inv = 1.f / powf(theta, static_cast<float>(2 * i) / static_cast<float>(D));
+    const float ang = static_cast<float>(pos) * inv;
+    c = cosf(ang);
+    s = sinf(ang);
+}
+
+// Fast GEMV: K == 512*KC, RW rows per wave (one wave per workgroup).
+template <int KC, int RW, int EPI, bool RMS>
+__global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
+    const int lane = threadIdx.x;
+    half8 xr[KC];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) xr[j] = load_half8(a.x + 512 * j + 8 * lane);
+    if constexpr (RMS) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = static_cast<float>(xr[j][e]);
+                ss = fmaf(v, v, ss);
+            }
+        ss = wave_sum_fast(ss);
+        const float rs = 1.f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const half8 w = load_half8(a.norm_w + 512 * j + 8 * lane);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                xr[j][e] = static_cast<f16>(static_cast<float>(xr[j][e]) * rs * static_cast<float>(w[e]));
+        }
+    }
+
+    // The rows of this wave.
+    int row[RW];
+    bool ok[RW];
+    const int wv = blockIdx.x;
+    if constexpr (EPI == kEpiQKV) {
+        // head hh, pair block pb: rows hh*D + 4pb + i and hh*D + D/2 + 4pb + i
+        const int wph = a.D / 8;
+        const int hh = wv / wph, pb = wv % wph;
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            row[i] = hh * a.D + (i < RW / 2 ? 0 : a.D / 2) + 4 * pb + (i % (RW / 2));
+            ok[i] = true;
+        }
+    } else if constexpr (EPI == kEpiSwiglu) {
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            const int n = wv * (RW / 2) + (i % (RW / 2));
+            ok[i] = n < a.N;
+            row[i] = (ok[i] ? n : 0) + (i < RW / 2 ? 0 : a.N);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            const int n = wv * RW + i;
+            ok[i] = n < a.N;
+            row[i] = ok[i] ? n : 0;
+        }
+    }
+
+    float acc[RW];
+    half8 wr[RW][KC];
+#pragma unroll
+    for (int i = 0; i < RW; ++i)
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+            wr[i][j] = load_half8_stream(a.W + (int64_t)row[i] * a.K + 512 * j + 8 * lane);
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+        acc[i] = 0.f;
+#pragma unroll
+        for (int j = 0; j < KC; ++j) acc[i] = dot8(wr[i][j], xr[j], acc[i]);
+        acc[i] = wave_sum_fast(acc[i]);
+    }
+
+    // Lane i (< RW) finishes row i (every lane holds every sum).
+    if constexpr (EPI == kEpiQKV) {
+        if (lane >= RW / 2) return;
+        float x1 = 0.f, x2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < RW / 2; ++i)
+            if (lane == i) {
+                x1 = round16(acc[i]);
+                x2 = round16(acc[RW / 2 + i]);
+            }
+        const int wph = a.D / 8;
+        const int hh = wv / wph, pb = wv % wph;
+        const int d = 4 * pb + lane;          // pair (d, d + D/2)
+        const int half = a.D / 2;
+        const int pos = a.seq_len[0] - 1;
+        if (hh >= a.Hq + a.Hkv) {             // v: no rotation
+            const int kvh = hh - a.Hq - a.Hkv;
+            if (pos < 0 || (pos >> 4) >= a.max_pages) return;
+            const int pid = a.bt[pos >> 4];
+            if (pid < 0 || pid >= a.num_pages) return;
+            f16* dst = a.pool_v + (((int64_t)kvh * a.num_pages + pid) * kPage + (pos & 15)) * a.D;
+            dst[d] = static_cast<f16>(x1);
+            dst[d + half] = static_cast<f16>(x2);
+            return;
+        }
+        float c, s;
+        rope_cs(pos < 0 ? 0 : pos, d, a.D, a.theta, c, s);
+        const f16 o1 = static_cast<f16>(x1 * c - x2 * s);
+        const f16 o2 = static_cast<f16>(x2 * c + x1 * s);
+        if (hh < a.Hq) {
+            a.y16[hh * a.D + d] = o1;
+            a.y16[hh * a.D + d + half] = o2;
+        } else {
+            const int kvh = hh - a.Hq;
+            if (pos < 0 || (pos >> 4) >= a.max_pages) return;
+            const int pid = a.bt[pos >> 4];
+            if (pid < 0 || pid >= a.num_pages) return;
+            f16* dst = a.pool_k + (((int64_t)kvh * a.num_pages + pid) * kPage + (pos & 15)) * a.D;
+            dst[d] = o1;
+            dst[d + half] = o2;
+        }
+    } else if constexpr (EPI == kEpiSwiglu) {
+        if (lane >= RW / 2) return;
+        float g = 0.f, u = 0.f;
+        bool valid = false;
+        int n = 0;
+#pragma unroll
+        for (int i = 0; i < RW / 2; ++i)
+            if (lane == i) {
+                g = round16(acc[i]);
+                u = round16(acc[RW / 2 + i]);
+                valid = ok[i];
+                n = row[i];
+            }
+        if (valid) a.y16[n] = static_cast<f16>(silu_mul(g, u));
+    } else {
+        if (lane >= RW) return;
+        float v = 0.f;
+        bool valid = false;
+        int n = 0;
+#pragma unroll
+        for (int i = 0; i < RW; ++i)
+            if (lane == i) {
+                v = acc[i];
+                valid = ok[i];
+                n = row[i];
+            }
+        if (!valid) return;
+        if constexpr (EPI == kEpiF32) {
+            a.y32[n] = v;
+        } else if constexpr (EPI == kEpiResidual) {
+            a.y16[n] = static_cast<f16>(v + static_cast<float>(a.resid[n]));
+        } else {
+            a.y16[n] = static_cast<f16>(v);
+        }
+    }
+}
+
+// Generic GEMV: one wave per output row (SwiGLU: per gate/up pair; QKV: per
+// rotation pair), any K.  RMSNorm prologue recomputed by every wave.
+template <int EPI, bool RMS>
+__global__ void __launch_bounds__(kWave) gemv_generic_kernel(const GemvArgs a) {
+    const int lane = threadIdx.x;
+    float rs = 1.f;
+    if constexpr (RMS) {
+        float ss = 0.f;
+        for (int k = lane; k < a.K; k += kWave) {
+            const float v = static_cast<float>(a.x[k]);
+            ss = fmaf(v, v, ss);
+        }
+        ss = wave_sum_fast(ss);
+        rs = 1.f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+    }
+    auto xin = [&](int k) {
+        if constexpr (RMS)
+            return static_cast<float>(static_cast<f16>(static_cast<float>(a.x[k]) * rs *
+                                                       static_cast<float>(a.norm_w[k])));
+        else
+            return static_cast<float>(a.x[k]);
+    };
+    auto dot_row = [&](int r) {
+        float acc = 0.f;
+        const f16* w = a.W + (int64_t)r * a.K;
+        for (int k = lane; k < a.K; k += kWave) acc = fmaf(static_cast<float>(w[k]), xin(k), acc);
+        return wave_sum_fast(acc);
+    };
+    const int t = blockIdx.x;
+    if constexpr (EPI == kEpiQKV) {
+        const int half = a.D / 2;
+        const int hh = t / half, d = t % half;
+        const float x1 = round16(dot_row(hh * a.D + d));
+        const float x2 = round16(dot_row(hh * a.D + d + half));
+        if (lane != 0) return;
+        const int pos = a.seq_len[0] - 1;
+        float o1 = x1, o2 = x2;
+        if (hh < a.Hq + a.Hkv) {
+            float c, s;
+            rope_cs(pos < 0 ? 0 : pos, d, a.D, a.theta, c, s);
+            o1 = x1 * c - x2 * s;
+            o2 = x2 * c + x1 * s;
+        }
+        if (hh < a.Hq) {
+            a.y16[hh * a.D + d] = static_cast<f16>(o1);
+            a.y16[hh * a.D + d + half] = static_cast<f16>(o2);
+            return;
+        }
+        if (pos < 0 || (pos >> 4) >= a.max_pages) return;
+        const int pid = a.bt[pos >> 4];
+        if (pid < 0 || pid >= a.num_pages) return;
+        const bool isk = hh < a.Hq + a.Hkv;
+        const int kvh = isk ? hh - a.Hq : hh - a.Hq - a.Hkv;
+        f16* dst = (isk ? a.pool_k : a.pool_v) +
+                   (((int64_t)kvh * a.num_pages + pid) * kPage + (pos & 15)) * a.D;
+        dst[d] = static_cast<f16>(o1);
+        dst[d + half] = static_cast<f16>(o2);
+    } else if constexpr (EPI == kEpiSwiglu) {
+        const float g = round16(dot_row(t));
+        const float u = round16(dot_row(a.N + t));
+        if (lane == 0) a.y16[t] = static_cast<f16>(silu_mul(g, u));
+    } else {
+        const float v = dot_row(t);
+        if (lane != 0) return;
+        if constexpr (EPI == kEpiF32)
+            a.y32[t] = v;
+        else if constexpr (EPI == kEpiResidual)
+            a.y16[t] = static_cast<f16>(v + static_cast<float>(a.resid[t]));
+        else
+            a.y16[t] = static_cast<f16>(v);
+    }
+}
+
+template <int EPI, bool RMS>
+int launch_gemv(const GemvArgs& a, hipStream_t s) {
+    int units;  // rows (or row pairs) the generic kernel runs one wave each on
+    if constexpr (EPI == kEpiQKV)
+        units = (a.Hq + 2 * a.Hkv) * (a.D / 2);
+    else
+        units = a.N;
+    const bool xa = aligned16(a.x) && aligned16(a.W) && (!RMS || aligned16(a.norm_w));
+    if (xa && a.K == 2048) {
+        constexpr int RW = 8;
+        int grid;
+        if constexpr (EPI == kEpiQKV)
+            grid = (a.Hq + 2 * a.Hkv) * (a.D / 8);
+        else if constexpr (EPI == kEpiSwiglu)
+            grid = (a.N + RW / 2 - 1) / (RW / 2);
+        else
+            grid = (a.N + RW - 1) / RW;
+        hipLaunchKernelGGL((gemv_kernel<4, RW, EPI, RMS>), dim3(grid), dim3(kWave), 0, s, a);
+    } else if (xa && a.K == 5632 && EPI != kEpiQKV && EPI != kEpiSwiglu) {
+        constexpr int RW = 4;
+        hipLaunchKernelGGL((gemv_kernel<11, RW, EPI, RMS>), dim3((a.N + RW - 1) / RW),
+                           dim3(kWave), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((gemv_generic_kernel<EPI, RMS>), dim3(units), dim3(kWave), 0, s, a);
+    }
+    return check_launch("gemv");
+}
+
+// Row-wise RMSNorm (prefill): one workgroup of 256 threads per row.
+__global__ void __launch_bounds__(256)
+rmsnorm_rows_kernel(const f16* x, const f16* w, f16* out, int dim, float eps) {
+    __shared__ float part[4];
+    const int64_t r = blockIdx.x;
+    const f16* xr = x + r * dim;
+    float ss = 0.f;
+    for (int k = threadIdx.x; k < dim; k += 256) {
+        const float v = static_cast<float>(xr[k]);
+        ss = fmaf(v, v, ss);
+    }
+    ss = wave_sum_fast(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = part[0] + part[1] + part[2] + part[3];
+    const float rs = 1.f / sqrtf(ss / static_cast<float>(dim) + eps);
+    for (int k = threadIdx.x; k < dim; k += 256)
+        out[r * dim + k] =
+            static_cast<f16>(static_cast<float>(xr[k]) * rs * static_cast<float>(w[k]));
+}
+
+// RoPE in place on token-major q [S][Hq][D] and k [S][Hkv][D] (reference
+// apply_rope, kernels.h:57-70): one thread per rotation pair.
+__global__ void rope_kernel(f16* q, f16* k, int64_t S, int Hq, int Hkv, int D, int start_pos,
+                            float theta) {
+    const int half = D / 2;
+    const int64_t pairs = S * (int64_t)(Hq + Hkv) * half;
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < pairs;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int i = static_cast<int>(t % half);
+        const int64_t sh = t / half;
+        const int h = static_cast<int>(sh % (Hq + Hkv));
+        const int64_t s = sh / (Hq + Hkv);
+        f16* v = h < Hq ? q + (s * Hq + h) * D : k + (s * Hkv + (h - Hq)) * D;
+        float c, sn;
+        rope_cs(static_cast<int>(start_pos + s), i, D, theta, c, sn);
+        const float x1 = static_cast<float>(v[i]), x2 = static_cast<float>(v[i + half]);
+        v[i] = static_cast<f16>(x1 * c - x2 * sn);
+        v[i + half] = static_cast<f16>(x2 * c + x1 * sn);
+    }
+}
+
+// Split the fused QKV projection [S][(Hq + 2Hkv) D] into contiguous q, k, v
+// with RoPE applied to q and k.
+__global__ void split_qkv_rope_kernel(const f16* qkv, int64_t S, int Hq, int Hkv, int D,
+                                      int start_pos, float theta, f16* q, f16* k, f16* v) {
+    const int half = D / 2;
+    const int H = Hq + 2 * Hkv;
+    const int64_t pairs = S * (int64_t)H * half;
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < pairs;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int i = static_cast<int>(t % half);
+        const int64_t sh = t / half;
+        const int h = static_cast<int>(sh % H);
+        const int64_t s = sh / H;
+        const f16* src = qkv + (s * H + h) * D;
+        const float x1 = static_cast<float>(src[i]), x2 = static_cast<float>(src[i + half]);
+        f16* dst;
+        float o1 = x1, o2 = x2;
+        if (h < Hq + Hkv) {
+            float c, sn;
+            rope_cs(static_cast<int>(start_pos + s), i, D, theta, c, sn);
+            o1 = x1 * c - x2 * sn;
+            o2 = x2 * c + x1 * sn;
+            dst = h < Hq ? q + (s * Hq + h) * D : k + (s * Hkv + (h - Hq)) * D;
+        } else {
+            dst = v + (s * Hkv + (h - Hq - Hkv)) * D;
+        }
+        dst[i] = static_cast<f16>(o1);
+        dst[i + half] = static_cast<f16>(o2);
+    }
+}
+
+// SwiGLU over rows of a fused [gate | up] buffer [rows][2n] -> out [rows][n];
+// with row stride 0 and n = count this is the reference's flat swiglu.
+__global__ void swiglu_kernel(const f16* gate, const f16* up, int64_t in_stride, f16* out,
+                              int64_t rows, int64_t n) {
+    const int64_t total = rows * n;
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = t / n, i = t % n;
+        const float g = static_cast<float>(gate[r * in_stride + i]);
+        const float u = static_cast<float>(up[r * in_stride + i]);
+        out[t] = static_cast<f16>(silu_mul(g, u));
+    }
+}
+
+// Embedding lookup: out[i][:] = table[ids[i]][:] (ids device int32; ids
+// outside [0, vocab) give zero rows).
+__global__ void embedding_kernel(const int32_t* ids, const f16* table, f16* out, int64_t n,
+                                 int64_t hidden, int64_t vocab) {
+    const int64_t i = blockIdx.x;
+    const int64_t id = ids[i];
+    for (int64_t k = threadIdx.x; k < hidden; k += blockDim.x)
+        out[i * hidden + k] = (id >= 0 && id < vocab) ? table[id * hidden + k] : static_cast<f16>(0.f);
+}
+
+// Greedy argmax of fp32 logits, lowest index on ties; NaN never wins.
+// Optionally appends the token to log[count] (count = *log_count, then
+// incremented) and advances *seq_len by one.
+__global__ void __launch_bounds__(1024)
+argmax_kernel(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, int32_t* log,
+              int32_t* log_count) {
+    __shared__ float bv[16];
+    __shared__ int64_t bi[16];
+    float best = -INFINITY;
+    int64_t idx = n;  // sentinel: larger than any index
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = logits[i];
+        if (v > best || (idx == n && !(v != v))) {  // first non-NaN, then strictly greater
+            best = v;
+            idx = i;
+        }
+    }
+    // wave reduction: larger value wins, equal values -> smaller index
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int64_t oi = __shfl_xor(idx, off);
+        if (ov > best || (ov == best && oi < idx) || (idx == n && oi < n)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        bv[w] = best;
+        bi[w] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int i = 1; i < static_cast<int>(blockDim.x >> 6); ++i)
+        if (bv[i] > best || (bv[i] == best && bi[i] < idx) || (idx == n && bi[i] < n)) {
+            best = bv[i];
+            idx = bi[i];
+        }
+    const int32_t tok = idx < n ? static_cast<int32_t>(idx) : 0;
+    *token = tok;
+    if (log) log[(*log_count)++] = tok;
+    if (seq_len) *seq_len += 1;
+}
+
+// Seeded N(0, std) fill: element i of stream `stream_id` is a Box-Muller
+// normal from two 64-bit splitmix hashes of (seed, stream_id, i).
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__global__ void randn_kernel(f16* out, int64_t n, uint64_t seed, uint64_t stream_id, float std) {
+    const uint64_t base = splitmix64(seed ^ splitmix64(stream_id));
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const uint64_t h1 = splitmix64(base + 2 * static_cast<uint64_t>(i));
+        const uint64_t h2 = splitmix64(base + 2 * static_cast<uint64_t>(i) + 1);
+        const float u1 = (static_cast<float>(h1 >> 40) + 0.5f) * (1.f / 16777216.f);  // (0, 1)
+        const float u2 = static_cast<float>(h2 >> 40) * (1.f / 16777216.f);          // [0, 1)
+        const float r = sqrtf(-2.f * logf(u1));
+        out[i] = static_cast<f16>(std * r * cospif(2.f * u2));
+    }
+}
+__global__ void fill_kernel(f16* out, int64_t n, float value) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = static_cast<f16>(value);
+}
+
+unsigned grid_for(int64_t n, int threads) {
+    int64_t g = (n + threads - 1) / threads;
+    if (g > 8192) g = 8192;
+    return static_cast<unsigned>(g < 1 ? 1 : g);
+}
+
+}  // namespace
+
+}  // namespace kvhp
+
+using namespace kvhp;
+
+namespace {
+GemvArgs gemv_args(const void* W, const void* x, int N, int K) {
+    GemvArgs a{};
+    a.W = static_cast<const f16*>(W);
+    a.x = static_cast<const f16*>(x);
+    a.N = N;
+    a.K = K;
+    return a;
+}
+int check_gemv(const void* W, const void* x, int N, int K, const char* what) {
+    KVHP_REQUIRE(W && x, KVHP_ERR_INVALID, "%s: null pointer", what);
+    KVHP_REQUIRE(N > 0 && K > 0, KVHP_ERR_INVALID, "%s: N=%d K=%d must be positive", what, N, K);
+    return KVHP_OK;
+}
+}  // namespace
+
+extern "C" int kvhp_gemv(const void* W, const void* x, void* y, int N, int K, void* stream) {
+    clear_error();
+    if (N == 0) return KVHP_OK;
+    int rc = check_gemv(W, x, N, K, "gemv");
+    if (rc) return rc;
+    KVHP_REQUIRE(y, KVHP_ERR_INVALID, "gemv: null output");
+    GemvArgs a = gemv_args(W, x, N, K);
+    a.y16 = static_cast<f16*>(y);
+    return launch_gemv<kEpiF16, false>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvhp_gemv_residual(const void* W, const void* x, const void* r, void* y, int N,
+                                  int K, void* stream) {
+    clear_error();
+    if (N == 0) return KVHP_OK;
+    int rc = check_gemv(W, x, N, K, "gemv_residual");
+    if (rc) return rc;
+    KVHP_REQUIRE(r && y, KVHP_ERR_INVALID, "gemv_residual: null residual/output");
+    GemvArgs a = gemv_args(W, x, N, K);
+    a.resid = static_cast<const f16*>(r);
+    a.y16 = static_cast<f16*>(y);
+    return launch_gemv<kEpiResidual, false>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvhp_rmsnorm_gemv(const void* W, const void* x, const void* norm_w, float eps,
+                                 void* y16, float* y32, int N, int K, void* stream) {
+    clear_error();
+    if (N == 0) return KVHP_OK;
+    int rc = check_gemv(W, x, N, K, "rmsnorm_gemv");
+    if (rc) return rc;
+    KVHP_REQUIRE(norm_w, KVHP_ERR_INVALID, "rmsnorm_gemv: null norm weight");
+    KVHP_REQUIRE((y16 != nullptr) != (y32 != nullptr), KVHP_ERR_INVALID,
+                 "rmsnorm_gemv: give exactly one of y16 / y32");
+    GemvArgs a = gemv_args(W, x, N, K);
+    a.norm_w = static_cast<const f16*>(norm_w);
+    a.eps = eps;
+    a.y16 = static_cast<f16*>(y16);
+    a.y32 = y32;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return y32 ? launch_gemv<kEpiF32, true>(a, s) : launch_gemv<kEpiF16, true>(a, s);
+}
+
+extern "C" int kvhp_rmsnorm_gemv_swiglu(const void* W_gate_up, const void* x, const void* norm_w,
+                                        float eps, void* out, int N, int K, void* stream) {
+    clear_error();
+    if (N == 0) return KVHP_OK;
+    int rc = check_gemv(W_gate_up, x, N, K, "rmsnorm_gemv_swiglu");
+    if (rc) return rc;
+    KVHP_REQUIRE(norm_w && out, KVHP_ERR_INVALID, "rmsnorm_gemv_swiglu: null pointer");
+    GemvArgs a = gemv_args(W_gate_up, x, N, K);
+    a.norm_w = static_cast<const f16*>(norm_w);
+    a.eps = eps;
+    a.y16 = static_cast<f16*>(out);
+    return launch_gemv<kEpiSwiglu, true>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvhp_rmsnorm_qkv_rope_append(const void* W_qkv, const void* x, const void* norm_w,
+                                            float eps, const int32_t* seq_len, float rope_theta,
+                                            void* q_out, void* pool_k, void* pool_v,
+                                            const int32_t* block_table, int max_pages,
+                                            int num_pages, int num_q_heads, int num_kv_heads,
+                                            int head_dim, int K, void* stream) {
+    clear_error();
+    const int N = (num_q_heads + 2 * num_kv_heads) * head_dim;
+    int rc = check_gemv(W_qkv, x, N, K, "rmsnorm_qkv_rope_append");
+    if (rc) return rc;
+    KVHP_REQUIRE(norm_w && seq_len && q_out && pool_k && pool_v && block_table, KVHP_ERR_INVALID,
+                 "rmsnorm_qkv_rope_append: null pointer");
+    KVHP_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 16 == 0,
+                 KVHP_ERR_INVALID, "rmsnorm_qkv_rope_append: head_dim %d must be a multiple of 16",
+                 head_dim);
+    KVHP_REQUIRE(max_pages > 0 && num_pages > 0, KVHP_ERR_INVALID,
+                 "rmsnorm_qkv_rope_append: empty page pool");
+    GemvArgs a = gemv_args(W_qkv, x, N, K);
+    a.norm_w = static_cast<const f16*>(norm_w);
+    a.eps = eps;
+    a.y16 = static_cast<f16*>(q_out);
+    a.Hq = num_q_heads;
+    a.Hkv = num_kv_heads;
+    a.D = head_dim;
+    a.seq_len = seq_len;
+    a.theta = rope_theta;
+    a.pool_k = static_cast<f16*>(pool_k);
+    a.pool_v = static_cast<f16*>(pool_v);
+    a.bt = block_table;
+    a.max_pages = max_pages;
+    a.num_pages = num_pages;
+    return launch_gemv<kEpiQKV, true>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvhp_rmsnorm(const void* x, const void* weight, void* out, int64_t rows,
+                            int64_t dim, float eps, void* stream) {
+    clear_error();
+    if (rows <= 0) return KVHP_OK;
+    KVHP_REQUIRE(x && weight && out && dim > 0 && dim <= (1 << 24), KVHP_ERR_INVALID,
+                 "rmsnorm: bad arguments");
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const f16*>(x),
+                       static_cast<const f16*>(weight), static_cast<f16*>(out),
+                       static_cast<int>(dim), eps);
+    return check_launch("rmsnorm");
+}
+
+extern "C" int kvhp_apply_rope(void* q, void* k, int64_t seq_len, int64_t num_q_heads,
+                               int64_t num_kv_heads, int64_t head_dim, int64_t start_pos,
+                               float rope_theta, void* stream) {
+    clear_error();
+    if (seq_len <= 0) return KVHP_OK;
+    KVHP_REQUIRE(q && k && head_dim > 0 && head_dim % 2 == 0 && num_q_heads > 0 &&
+                     num_kv_heads > 0,
+                 KVHP_ERR_INVALID, "apply_rope: bad arguments");
+    const int64_t pairs = seq_len * (num_q_heads + num_kv_heads) * (head_dim / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<f16*>(q),
+                       static_cast<f16*>(k), seq_len, static_cast<int>(num_q_heads),
+                       static_cast<int>(num_kv_heads), static_cast<int>(head_dim),
+                       static_cast<int>(start_pos), rope_theta);
+    return check_launch("apply_rope");
+}
+
+extern "C" int kvhp_split_qkv_rope(const void* qkv, int64_t seq_len, int num_q_heads,
+                                   int num_kv_heads, int head_dim, int64_t start_pos,
+                                   float rope_theta, void* q, void* k, void* v, void* stream) {
+    clear_error();
+    if (seq_len <= 0) return KVHP_OK;
+    KVHP_REQUIRE(qkv && q && k && v && head_dim > 0 && head_dim % 2 == 0 && num_q_heads > 0 &&
+                     num_kv_heads > 0,
+                 KVHP_ERR_INVALID, "split_qkv_rope: bad arguments");
+    const int64_t pairs = seq_len * (num_q_heads + 2 * num_kv_heads) * (head_dim / 2);
+    hipLaunchKernelGGL(split_qkv_rope_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const f16*>(qkv), seq_len,
+                       num_q_heads, num_kv_heads, head_dim, static_cast<int>(start_pos),
+                       rope_theta, static_cast<f16*>(q), static_cast<f16*>(k),
+                       static_cast<f16*>(v));
+    return check_launch("split_qkv_rope");
+}
+
+extern "C" int kvhp_swiglu(const void* gate, const void* up, void* out, int64_t count,
+                           void* stream) {
+    clear_error();
+    if (count <= 0) return KVHP_OK;
+    KVHP_REQUIRE(gate && up && out, KVHP_ERR_INVALID, "swiglu: null pointer");
+    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(count, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const f16*>(gate),
+                       static_cast<const f16*>(up), (int64_t)0, static_cast<f16*>(out),
+                       (int64_t)1, count);
+    return check_launch("swiglu");
+}
+
+extern "C" int kvhp_swiglu_rows(const void* gate_up, void* out, int64_t rows, int64_t n,
+                                void* stream) {
+    clear_error();
+    if (rows <= 0 || n <= 0) return KVHP_OK;
+    KVHP_REQUIRE(gate_up && out, KVHP_ERR_INVALID, "swiglu_rows: null pointer");
+    const f16* g = static_cast<const f16*>(gate_up);
+    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(rows * n, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), g, g + n, 2 * n, static_cast<f16*>(out),
+                       rows, n);
+    return check_launch("swiglu_rows");
+}
+
+extern "C" int kvhp_embedding(const int32_t* token_ids, const void* table, void* out, int64_t n,
+                              int64_t hidden, int64_t vocab, void* stream) {
+    clear_error();
+    if (n <= 0) return KVHP_OK;
+    KVHP_REQUIRE(token_ids && table && out && hidden > 0 && vocab > 0, KVHP_ERR_INVALID,
+                 "embedding: bad arguments");
+    hipLaunchKernelGGL(embedding_kernel, dim3(static_cast<unsigned>(n)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), token_ids,
+                       static_cast<const f16*>(table), static_cast<f16*>(out), n, hidden, vocab);
+    return check_launch("embedding");
+}
+
+extern "C" int kvhp_argmax(const float* logits, int64_t n, int32_t* token, int32_t* seq_len,
+                           int32_t* log, int32_t* log_count, void* stream) {
+    clear_error();
+    KVHP_REQUIRE(logits && token && n > 0 && n < (int64_t)1 << 31, KVHP_ERR_INVALID,
+                 "argmax: bad arguments");
+    KVHP_REQUIRE((log == nullptr) == (log_count == nullptr), KVHP_ERR_INVALID,
+                 "argmax: log and log_count go together");
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                       logits, n, token, seq_len, log, log_count);
+    return check_launch("argmax");
+}
+
+extern "C" int kvhp_randn_f16(void* out, int64_t count, uint64_t seed, uint64_t stream_id,
+                              float std_dev, void* stream) {
+    clear_error();
+    if (count <= 0) return KVHP_OK;
+    KVHP_REQUIRE(out, KVHP_ERR_INVALID, "randn: null output");
+    hipLaunchKernelGGL(randn_kernel, dim3(grid_for(count, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<f16*>(out), count, seed,
+                       stream_id, std_dev);
+    return check_launch("randn_f16");
+}
+
+extern "C" int kvhp_fill_f16(void* out, int64_t count, float value, void* stream) {
+    clear_error();
+    if (count <= 0) return KVHP_OK;
+    KVHP_REQUIRE(out, KVHP_ERR_INVALID, "fill: null output");
+    hipLaunchKernelGGL(fill_kernel, dim3(grid_for(count, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<f16*>(out), count, value);
+    return check_launch("fill_f16");
+}

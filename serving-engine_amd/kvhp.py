@@ -55,6 +55,8 @@ _vp = ctypes.c_void_p
 _i32 = ctypes.c_int
 _i64 = ctypes.c_int64
 _sz = ctypes.c_size_t
+_f32 = ctypes.c_float
+_u64 = ctypes.c_uint64
 
 # name -> (restype, argtypes)
 _SIGNATURES = {
@@ -75,6 +77,22 @@ _SIGNATURES = {
     "kvhp_flash_prefill_paged": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp,
                                         _vp, _vp, _i32, _i32, _vp]),
     "kvhp_causal_gqa": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    # model operators
+    "kvhp_gemv": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp]),
+    "kvhp_gemv_residual": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp]),
+    "kvhp_rmsnorm_gemv": (_i32, [_vp, _vp, _vp, _f32, _vp, _vp, _i32, _i32, _vp]),
+    "kvhp_rmsnorm_gemv_swiglu": (_i32, [_vp, _vp, _vp, _f32, _vp, _i32, _i32, _vp]),
+    "kvhp_rmsnorm_qkv_rope_append": (_i32, [_vp, _vp, _vp, _f32, _vp, _f32, _vp, _vp, _vp, _vp,
+                                            _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "kvhp_rmsnorm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
+    "kvhp_apply_rope": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp]),
+    "kvhp_split_qkv_rope": (_i32, [_vp, _i64, _i32, _i32, _i32, _i64, _f32, _vp, _vp, _vp, _vp]),
+    "kvhp_swiglu": (_i32, [_vp, _vp, _vp, _i64, _vp]),
+    "kvhp_swiglu_rows": (_i32, [_vp, _vp, _i64, _i64, _vp]),
+    "kvhp_embedding": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "kvhp_argmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "kvhp_randn_f16": (_i32, [_vp, _i64, _u64, _u64, _f32, _vp]),
+    "kvhp_fill_f16": (_i32, [_vp, _i64, _f32, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -223,3 +241,73 @@ def flash_prefill_paged(q, k, v, out, seq_len, num_q_heads, num_kv_heads, head_d
 def causal_gqa(q, k, v, out, seq_len, num_q_heads, num_kv_heads, head_dim, stream=None):
     _check(load().kvhp_causal_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(out), seq_len, num_q_heads,
                                   num_kv_heads, head_dim, _stream(stream)))
+
+
+# ------------------------------------------------------ model operators --
+def gemv(W, x, y, N, K, stream=None):
+    _check(load().kvhp_gemv(_ptr(W), _ptr(x), _ptr(y), N, K, _stream(stream)))
+
+
+def gemv_residual(W, x, r, y, N, K, stream=None):
+    _check(load().kvhp_gemv_residual(_ptr(W), _ptr(x), _ptr(r), _ptr(y), N, K, _stream(stream)))
+
+
+def rmsnorm_gemv(W, x, norm_w, eps, N, K, y16=None, y32=None, stream=None):
+    _check(load().kvhp_rmsnorm_gemv(_ptr(W), _ptr(x), _ptr(norm_w), eps, _ptr(y16), _ptr(y32), N,
+                                    K, _stream(stream)))
+
+
+def rmsnorm_gemv_swiglu(W_gate_up, x, norm_w, eps, out, N, K, stream=None):
+    _check(load().kvhp_rmsnorm_gemv_swiglu(_ptr(W_gate_up), _ptr(x), _ptr(norm_w), eps, _ptr(out),
+                                           N, K, _stream(stream)))
+
+
+def rmsnorm_qkv_rope_append(W_qkv, x, norm_w, eps, seq_len, theta, q_out, pool_k, pool_v,
+                            block_table, num_q_heads, num_kv_heads, head_dim, K, stream=None):
+    """pool_k / pool_v [Hkv][P][16][D]; block_table int32 [max_pages] (one sequence)."""
+    _check(load().kvhp_rmsnorm_qkv_rope_append(
+        _ptr(W_qkv), _ptr(x), _ptr(norm_w), eps, _ptr(seq_len), theta, _ptr(q_out), _ptr(pool_k),
+        _ptr(pool_v), _ptr(block_table), block_table.numel(), pool_k.shape[1], num_q_heads,
+        num_kv_heads, head_dim, K, _stream(stream)))
+
+
+def rmsnorm(x, weight, out, rows, dim, eps, stream=None):
+    _check(load().kvhp_rmsnorm(_ptr(x), _ptr(weight), _ptr(out), rows, dim, eps, _stream(stream)))
+
+
+def apply_rope(q, k, seq_len, num_q_heads, num_kv_heads, head_dim, start_pos, theta, stream=None):
+    _check(load().kvhp_apply_rope(_ptr(q), _ptr(k), seq_len, num_q_heads, num_kv_heads, head_dim,
+                                  start_pos, theta, _stream(stream)))
+
+
+def split_qkv_rope(qkv, seq_len, num_q_heads, num_kv_heads, head_dim, start_pos, theta, q, k, v,
+                   stream=None):
+    _check(load().kvhp_split_qkv_rope(_ptr(qkv), seq_len, num_q_heads, num_kv_heads, head_dim,
+                                      start_pos, theta, _ptr(q), _ptr(k), _ptr(v),
+                                      _stream(stream)))
+
+
+def swiglu(gate, up, out, count, stream=None):
+    _check(load().kvhp_swiglu(_ptr(gate), _ptr(up), _ptr(out), count, _stream(stream)))
+
+
+def swiglu_rows(gate_up, out, rows, n, stream=None):
+    _check(load().kvhp_swiglu_rows(_ptr(gate_up), _ptr(out), rows, n, _stream(stream)))
+
+
+def embedding(token_ids, table, out, n, hidden, vocab, stream=None):
+    _check(load().kvhp_embedding(_ptr(token_ids), _ptr(table), _ptr(out), n, hidden, vocab,
+                                 _stream(stream)))
+
+
+def argmax(logits, n, token, seq_len=None, log=None, log_count=None, stream=None):
+    _check(load().kvhp_argmax(_ptr(logits), n, _ptr(token), _ptr(seq_len), _ptr(log),
+                              _ptr(log_count), _stream(stream)))
+
+
+def randn_f16(out, seed, stream_id, std, stream=None):
+    _check(load().kvhp_randn_f16(_ptr(out), out.numel(), seed, stream_id, std, _stream(stream)))
+
+
+def fill_f16(out, value, stream=None):
+    _check(load().kvhp_fill_f16(_ptr(out), out.numel(), value, _stream(stream)))

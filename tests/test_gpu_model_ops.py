@@ -1,0 +1,241 @@
+"""GPU parity of the model operators (serving-engine_amd/csrc/model_ops.hip)
+against the oracle's restatement of the reference CPU ops (src/cpu/ops.cpp:
+RMSNorm :26-51, matmul :53-114, RoPE :165-221, SwiGLU :286-297).
+
+As in the reference's own kernel tests (docs/GATES.md: ">= 20 random shapes
+including sizes that are not tile multiples and length-1 sequences"), every
+op runs on random shapes that include the config-5 sizes (K = 2048, 5632)
+and odd ones.  The reference GPU path stores each projection and the RMSNorm
+output in fp16, so the oracle side rounds at the same points.  Tolerance:
+|g - r| <= 1e-3 + 2e-3 |r| per element (fp16 output rounding plus fp32 vs
+double accumulation order).
+"""
+import numpy as np
+import pytest
+
+import kvhp
+import oracle
+from gpu_util import to_gpu
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+ATOL, RTOL = 1e-3, 2e-3
+
+
+def _close(got, ref, what):
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    err = np.abs(got - ref)
+    bad = err > ATOL + RTOL * np.abs(ref)
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} out of tolerance, max abs {err.max():.3g}"
+
+
+def _f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def _cpu(t):
+    return t.float().cpu().numpy()
+
+
+GEMV_SHAPES = [(1, 8), (7, 24), (64, 512), (100, 2048), (2048, 2048), (2560, 2048), (33, 5632),
+               (2048, 5632), (300, 1000), (5, 2056), (129, 4096), (17, 64), (513, 2048),
+               (32000, 2048), (1, 2048), (8, 5632), (250, 136), (96, 3000), (4, 16), (3, 520)]
+
+
+@pytest.mark.parametrize("n,k", GEMV_SHAPES)
+def test_gemv_and_residual(n, k):
+    rng = np.random.default_rng(n * 7919 + k)
+    W = oracle.normal_f16(rng, (n, k), 0.02)
+    x = oracle.normal_f16(rng, (k,))
+    r = oracle.normal_f16(rng, (n,))
+    ref = oracle.matmul_transB(x[None, :].astype(np.float32), W.astype(np.float32), nthreads=8)[0]
+    Wd, xd, rd = to_gpu(W), to_gpu(x), to_gpu(r)
+    y = torch.empty(n, dtype=torch.float16, device="cuda")
+    kvhp.gemv(Wd, xd, y, n, k)
+    torch.cuda.synchronize()
+    _close(_cpu(y), _f16(ref), f"gemv {n}x{k}")
+    y2 = rd.clone()  # in place: y = W x + y
+    kvhp.gemv_residual(Wd, xd, y2, y2, n, k)
+    torch.cuda.synchronize()
+    _close(_cpu(y2), _f16(ref + r.astype(np.float32)), f"gemv_residual {n}x{k}")
+
+
+@pytest.mark.parametrize("n,k", [(64, 512), (2048, 2048), (32000, 2048), (100, 5632), (9, 40)])
+def test_rmsnorm_gemv(n, k):
+    rng = np.random.default_rng(n + 31 * k)
+    W = oracle.normal_f16(rng, (n, k), 0.02)
+    x = oracle.normal_f16(rng, (k,))
+    w = (1.0 + oracle.normal_f16(rng, (k,), 0.1).astype(np.float32)).astype(np.float16)
+    xn = _f16(oracle.rmsnorm(x[None, :], w, 1e-5))
+    ref = oracle.matmul_transB(xn, W.astype(np.float32), nthreads=8)[0]
+    Wd, xd, wd = to_gpu(W), to_gpu(x), to_gpu(w)
+    y16 = torch.empty(n, dtype=torch.float16, device="cuda")
+    y32 = torch.empty(n, dtype=torch.float32, device="cuda")
+    kvhp.rmsnorm_gemv(Wd, xd, wd, 1e-5, n, k, y16=y16)
+    kvhp.rmsnorm_gemv(Wd, xd, wd, 1e-5, n, k, y32=y32)
+    torch.cuda.synchronize()
+    _close(_cpu(y16), _f16(ref), "rmsnorm_gemv fp16")
+    _close(y32.cpu().numpy(), ref, "rmsnorm_gemv fp32")
+
+
+@pytest.mark.parametrize("n,k", [(5632, 2048), (64, 2048), (37, 2048), (100, 320), (1, 2048)])
+def test_rmsnorm_gemv_swiglu(n, k):
+    rng = np.random.default_rng(n * 3 + k)
+    Wgu = oracle.normal_f16(rng, (2 * n, k), 0.02)
+    x = oracle.normal_f16(rng, (k,))
+    w = np.ones(k, np.float16)
+    xn = _f16(oracle.rmsnorm(x[None, :], w, 1e-5))
+    gu = _f16(oracle.matmul_transB(xn, Wgu.astype(np.float32), nthreads=8)[0])
+    ref = oracle.swiglu(gu[:n], gu[n:])
+    out = torch.empty(n, dtype=torch.float16, device="cuda")
+    kvhp.rmsnorm_gemv_swiglu(to_gpu(Wgu), to_gpu(x), to_gpu(w), 1e-5, out, n, k)
+    torch.cuda.synchronize()
+    _close(_cpu(out), _f16(ref), f"rmsnorm_gemv_swiglu {n}x{k}")
+
+
+@pytest.mark.parametrize("hq,hkv,d,k,pos", [(32, 4, 64, 2048, 0), (32, 4, 64, 2048, 2175),
+                                           (8, 2, 128, 2048, 37), (4, 4, 64, 256, 5),
+                                           (6, 2, 32, 96, 16)])
+def test_rmsnorm_qkv_rope_append(hq, hkv, d, k, pos):
+    rng = np.random.default_rng(hq * 100 + pos)
+    n = (hq + 2 * hkv) * d
+    W = oracle.normal_f16(rng, (n, k), 0.02)
+    x = oracle.normal_f16(rng, (k,))
+    w = (1.0 + oracle.normal_f16(rng, (k,), 0.1).astype(np.float32)).astype(np.float16)
+    theta = 10000.0
+    # oracle: fp16 norm output, fp16 projection, RoPE in fp32, fp16 again
+    xn = _f16(oracle.rmsnorm(x[None, :], w, 1e-5))
+    qkv = _f16(oracle.matmul_transB(xn, W.astype(np.float32), nthreads=8)[0])
+    q, kk = oracle.apply_rope(qkv[:hq * d], qkv[hq * d:(hq + hkv) * d], hq, hkv, d, pos, theta)
+    v = qkv[(hq + hkv) * d:]
+    P = pos // 16 + 3
+    perm = np.random.default_rng(pos).permutation(P).astype(np.int32)
+    pool_k = torch.zeros((hkv, P, 16, d), dtype=torch.float16, device="cuda")
+    pool_v = torch.zeros_like(pool_k)
+    q_out = torch.empty(hq * d, dtype=torch.float16, device="cuda")
+    seq_len = torch.tensor([pos + 1], dtype=torch.int32, device="cuda")
+    kvhp.rmsnorm_qkv_rope_append(to_gpu(W), to_gpu(x), to_gpu(w), 1e-5, seq_len, theta, q_out,
+                                 pool_k, pool_v, torch.from_numpy(perm).cuda(), hq, hkv, d, k)
+    torch.cuda.synchronize()
+    _close(_cpu(q_out), _f16(q), "q")
+    page, slot = perm[pos // 16], pos % 16
+    pk = pool_k.float().cpu().numpy()
+    pv = pool_v.float().cpu().numpy()
+    _close(pk[:, page, slot, :].reshape(-1), _f16(kk), "k page")
+    _close(pv[:, page, slot, :].reshape(-1), v, "v page")
+    # nothing else in the pools was written
+    mask = np.ones(pk.shape[1:3], bool)
+    mask[page, slot] = False
+    assert not pk[:, mask].any() and not pv[:, mask].any()
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 2048), (2048, 2048), (7, 100), (3, 5632), (65, 64)])
+def test_rmsnorm_rows(rows, dim):
+    rng = np.random.default_rng(rows + dim)
+    x = oracle.normal_f16(rng, (rows, dim))
+    w = (1.0 + oracle.normal_f16(rng, (dim,), 0.1).astype(np.float32)).astype(np.float16)
+    ref = oracle.rmsnorm(x, w, 1e-5)
+    out = torch.empty((rows, dim), dtype=torch.float16, device="cuda")
+    kvhp.rmsnorm(to_gpu(x), to_gpu(w), out, rows, dim, 1e-5)
+    torch.cuda.synchronize()
+    _close(_cpu(out), _f16(ref), "rmsnorm rows")
+
+
+@pytest.mark.parametrize("s,hq,hkv,d,start", [(1, 32, 4, 64, 0), (2048, 32, 4, 64, 0),
+                                             (17, 8, 2, 128, 100), (5, 6, 3, 32, 2047)])
+def test_rope_and_split_qkv(s, hq, hkv, d, start):
+    rng = np.random.default_rng(s + start)
+    qkv = oracle.normal_f16(rng, (s, hq + 2 * hkv, d))
+    q = np.ascontiguousarray(qkv[:, :hq])
+    k = np.ascontiguousarray(qkv[:, hq:hq + hkv])
+    v = np.ascontiguousarray(qkv[:, hq + hkv:])
+    rq, rk = oracle.apply_rope(q, k, hq, hkv, d, start, 10000.0)
+    qd, kd = to_gpu(q), to_gpu(k)
+    kvhp.apply_rope(qd, kd, s, hq, hkv, d, start, 10000.0)
+    q2 = torch.empty_like(qd)
+    k2 = torch.empty_like(kd)
+    v2 = torch.empty((s, hkv, d), dtype=torch.float16, device="cuda")
+    kvhp.split_qkv_rope(to_gpu(qkv), s, hq, hkv, d, start, 10000.0, q2, k2, v2)
+    torch.cuda.synchronize()
+    for got, ref, what in ((qd, rq, "rope q"), (kd, rk, "rope k"), (q2, rq, "split q"),
+                           (k2, rk, "split k")):
+        _close(_cpu(got).reshape(-1), _f16(ref).reshape(-1), what)
+    assert np.array_equal(_cpu(v2), v.astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,n", [(1, 5632), (2048, 5632), (3, 7)])
+def test_swiglu(rows, n):
+    rng = np.random.default_rng(rows * n)
+    gu = oracle.normal_f16(rng, (rows, 2 * n), 2.0)
+    ref = oracle.swiglu(gu[:, :n], gu[:, n:])
+    out = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+    kvhp.swiglu_rows(to_gpu(gu), out, rows, n)
+    flat = torch.empty(rows * n, dtype=torch.float16, device="cuda")
+    g = to_gpu(np.ascontiguousarray(gu[:, :n]))
+    u = to_gpu(np.ascontiguousarray(gu[:, n:]))
+    kvhp.swiglu(g, u, flat, rows * n)
+    torch.cuda.synchronize()
+    _close(_cpu(out), _f16(ref), "swiglu rows")
+    _close(_cpu(flat).reshape(rows, n), _f16(ref), "swiglu flat")
+
+
+def test_embedding():
+    rng = np.random.default_rng(5)
+    vocab, hidden = 1000, 2048
+    table = oracle.normal_f16(rng, (vocab, hidden), 0.02)
+    ids = np.array([0, 999, 5, 5, -1, 1000, 123], np.int32)
+    out = torch.empty((ids.size, hidden), dtype=torch.float16, device="cuda")
+    kvhp.embedding(torch.from_numpy(ids).cuda(), to_gpu(table), out, ids.size, hidden, vocab)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for i, t in enumerate(ids):
+        exp = table[t] if 0 <= t < vocab else np.zeros(hidden, np.float16)
+        assert np.array_equal(got[i].view(np.uint16), exp.view(np.uint16)), i
+
+
+def test_argmax_ties_nan_and_counters():
+    rng = np.random.default_rng(9)
+    cases = []
+    x = rng.standard_normal(32000).astype(np.float32)
+    cases.append((x.copy(), int(np.argmax(x))))
+    y = x.copy()
+    y[[7, 30000, 123]] = 50.0                   # tie: lowest index wins
+    cases.append((y, 7))
+    z = x.copy()
+    z[[3, 10]] = np.nan
+    z[31999] = 60.0                              # NaN never wins
+    cases.append((z, 31999))
+    w = np.full(5, -np.inf, np.float32)          # all -inf -> index 0
+    cases.append((w, 0))
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    seq = torch.tensor([10], dtype=torch.int32, device="cuda")
+    log = torch.full((8,), -1, dtype=torch.int32, device="cuda")
+    cnt = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for logits, want in cases:
+        kvhp.argmax(torch.from_numpy(logits).cuda(), logits.size, tok, seq, log, cnt)
+        torch.cuda.synchronize()
+        assert int(tok.item()) == want
+    assert int(seq.item()) == 10 + len(cases)
+    assert int(cnt.item()) == len(cases)
+    assert log.cpu().numpy()[:len(cases)].tolist() == [c[1] for c in cases]
+
+
+def test_randn_and_fill():
+    a = torch.empty(1 << 20, dtype=torch.float16, device="cuda")
+    b = torch.empty_like(a)
+    c = torch.empty_like(a)
+    kvhp.randn_f16(a, 1234, 7, 0.02)
+    kvhp.randn_f16(b, 1234, 7, 0.02)
+    kvhp.randn_f16(c, 1234, 8, 0.02)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)                     # deterministic
+    assert not torch.equal(a, c)                 # streams differ
+    v = a.float().cpu().numpy()
+    assert abs(v.mean()) < 2e-4 and abs(v.std() - 0.02) < 2e-4
+    assert abs(np.mean(np.abs(v) < 0.02) - 0.6827) < 0.005
+    kvhp.fill_f16(a, 1.0)
+    torch.cuda.synchronize()
+    assert bool((a == 1.0).all())
