@@ -19,7 +19,9 @@ oracle's restatement of the reference CPU attention arithmetic
 Also reported under "extra" (each measured with L2+MALL flushed by a 1 GiB
 read before every rep unless labelled warm): config 1 (decode at ctx 512),
 config 2 (ctx 4K/16K/64K x splits 1/4/16/64), config 4 (causal prefill
-S=512/2048/8192, TFLOP/s vs fp16 MFMA peak).
+S=512/2048/8192, TFLOP/s vs fp16 MFMA peak), config 5 (Llama-style 1.1B:
+2048-id prefill, then 128 greedy decode steps, tok/s and the HBM bytes of a
+step against 8 TB/s; also top-level as config5_decode_tok_s).
 """
 import argparse
 import json
@@ -49,7 +51,7 @@ def parse():
     ap.add_argument("--splits", type=int, default=0, help="decode split count (0 = auto)")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 2 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4")
+    ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5")
     ap.add_argument("--profile", nargs="?", const="decode", default=None,
                     choices=("decode", "prefill"),
                     help="short run for rocprofv3: a 256 MiB device copy (counter "
@@ -303,6 +305,54 @@ def run_config4(torch, kvhp, sizes=(512, 2048, 8192), reps=10):
             "rows": rows}
 
 
+def config5_step_bytes(cfg, ctx):
+    """HBM bytes of one batch-1 decode step at context ctx: every weight once
+    (fused q/k/v, o, gate/up, down per layer; LM head; one embedding row;
+    norm vectors), the K/V cache of all layers, the new K/V rows."""
+    h, d, hq, hkv, f, v, L = (cfg.hidden_size, cfg.head_dim, cfg.num_q_heads, cfg.num_kv_heads,
+                              cfg.ffn_size, cfg.vocab_size, cfg.num_layers)
+    per_layer = ((hq + 2 * hkv) * d * h + h * hq * d + 2 * f * h + h * f + 2 * h) * 2
+    kv = L * 2 * hkv * d * 2 * ctx
+    return L * per_layer + v * h * 2 + h * 2 + h * 2 + kv
+
+
+def run_config5(torch, kvhp, steps=128, prompt_len=2048):
+    """random-init Llama-style 1.1B, seeded 2048-id prompt,
+    prefill then `steps` greedy decode steps (HIP graph of the step)."""
+    cfg = kvhp.llama_1b_config()
+    model = kvhp.LlamaModel(cfg, seed=5, max_ctx=prompt_len + steps + 1)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, prompt_len).astype(np.int32)
+    model.prefill(prompt[:16])                     # warm the library paths (rocBLAS, kernels)
+    model.close()
+    model = kvhp.LlamaModel(cfg, seed=5, max_ctx=prompt_len + steps + 1)
+    t0 = time.perf_counter()
+    first, _ = model.prefill(prompt)
+    prefill_s = time.perf_counter() - t0
+    toks, ms = model.generate(steps, use_graph=True)
+    model.close()
+    # same work launched kernel by kernel (no graph), for the launch-overhead picture
+    model = kvhp.LlamaModel(cfg, seed=5, max_ctx=prompt_len + steps + 1)
+    model.prefill(prompt)
+    toks2, ms_eager = model.generate(steps, use_graph=False)
+    model.close()
+    assert toks[:steps + 1].tolist() == toks2[:steps + 1].tolist(), "graph and eager tokens differ"
+    tok_s = steps / (ms / 1e3)
+    mean_ctx = prompt_len + (steps + 1) / 2
+    nb = config5_step_bytes(cfg, mean_ctx)
+    gbps = nb * tok_s / 1e9
+    return {"workload": "config5: Llama-style 1.1B (22 x [H 2048, 32/4 heads of 64, SwiGLU 5632], "
+                        "vocab 32000, untied LM head, fp16 N(0,0.02) weights, norms 1), seeded "
+                        f"{prompt_len}-id prompt, {steps} greedy steps, batch 1, HIP graph per step",
+            "decode_tok_s": round(tok_s, 1), "ms_per_token": round(ms / steps, 4),
+            "decode_tok_s_no_graph": round(steps / (ms_eager / 1e3), 1),
+            "prefill_ms": round(prefill_s * 1e3, 2),
+            "prefill_tok_s": round(prompt_len / prefill_s, 1),
+            "bytes_per_token": nb, "achieved_GBps": round(gbps, 1),
+            "pct_hbm_peak": round(gbps / HBM_PEAK_GBS * 100, 2),
+            "roofline_tok_s_at_8TBps": round(HBM_PEAK_GBS * 1e9 / nb, 1),
+            "first_tokens": toks[:8].tolist()}
+
+
 def traffic_from_profile(dbytes):
     """HBM bytes per decode call from the committed rocprofv3 --pmc summary
     (profiles/decode_config3_traffic.json), if present."""
@@ -385,7 +435,7 @@ def main():
     del c
     torch.cuda.empty_cache()
     extra = {}
-    parts = set(args.only.split(",")) if args.only else {"c1", "c2", "c4"}
+    parts = set(args.only.split(",")) if args.only else {"c1", "c2", "c4", "c5"}
     if not args.no_extra:
         if "c1" in parts:
             log("config1 ...")
@@ -396,6 +446,10 @@ def main():
         if "c4" in parts:
             log("config4 ...")
             extra["config4"] = run_config4(torch, kvhp)
+        if "c5" in parts:
+            log("config5 ...")
+            extra["config5"] = run_config5(torch, kvhp)
+            line["config5_decode_tok_s"] = extra["config5"]["decode_tok_s"]
     line["extra"] = extra
     print(json.dumps(line))
 

@@ -231,6 +231,60 @@ int kvhp_randn_f16(void* out, int64_t count, uint64_t seed, uint64_t stream_id, 
 /* Constant fp16 fill. */
 int kvhp_fill_f16(void* out, int64_t count, float value, void* stream);
 
+/* ---- Decoder-only model runner (config 5: Llama-style, batch 1), the
+ * reference's model entry points prefill_gpu / decode_step_gpu
+ * (src/model/forward_gpu.h:88-113) over this library's kernels.  Weights are
+ * synthetic: every matrix N(0, 0.02) fp16 from kvhp_randn_f16 with the given
+ * seed (one stream id per tensor, in creation order), RMSNorm weights 1; the
+ * LM head is untied; no projection biases. ---------------------------------- */
+typedef struct kvhp_llama_config {
+    int vocab_size;
+    int hidden_size;
+    int num_layers;
+    int num_q_heads;
+    int num_kv_heads;
+    int head_dim;
+    int ffn_size;
+    float rms_eps;
+    float rope_theta;
+    int reserved;
+} kvhp_llama_config;
+
+/* Tensor ids for kvhp_llama_tensor (layer < 0: model-level tensors). */
+#define KVHP_LLAMA_EMBED 0       /* [V][H]                         */
+#define KVHP_LLAMA_LM_HEAD 1     /* [V][H]                         */
+#define KVHP_LLAMA_FINAL_NORM 2  /* [H]                            */
+#define KVHP_LLAMA_ATTN_NORM 10  /* [H]                            */
+#define KVHP_LLAMA_FFN_NORM 11   /* [H]                            */
+#define KVHP_LLAMA_W_QKV 12      /* [(Hq + 2 Hkv) D][H]: q; k; v   */
+#define KVHP_LLAMA_W_O 13        /* [H][Hq D]                      */
+#define KVHP_LLAMA_W_GATE_UP 14  /* [2F][H]: gate; up              */
+#define KVHP_LLAMA_W_DOWN 15     /* [H][F]                         */
+#define KVHP_LLAMA_POOL_K 16     /* [Hkv][P][16][D] KV pages       */
+#define KVHP_LLAMA_POOL_V 17
+
+/* Allocate and initialise a model for contexts up to max_ctx tokens. */
+int kvhp_llama_create(const kvhp_llama_config* config, uint64_t seed, int max_ctx,
+                      void** model);
+int kvhp_llama_destroy(void* model);
+/* prefill_gpu (forward_gpu.h:93-101): n prompt ids (host), K/V of every
+ * position into the pages; logits_out (host, V floats, may be NULL) of the
+ * last position; *next_token = its greedy argmax. */
+int kvhp_llama_prefill(void* model, const int32_t* tokens, int n, float* logits_out,
+                       int32_t* next_token);
+/* decode_step_gpu (forward_gpu.h:103-113): one token at the next position.
+ * token < 0 continues from the last greedy token; token >= 0 replaces it
+ * (teacher forcing).  logits_out (host) and *next_token as for prefill. */
+int kvhp_llama_decode_step(void* model, int32_t token, float* logits_out, int32_t* next_token);
+/* n_steps greedy decode steps entirely on the device (use_graph: captured
+ * once as a HIP graph, replayed per step).  tokens_out (host) receives every
+ * token generated since the prefill (its argmax first); *elapsed_ms the
+ * device time of the n_steps steps. */
+int kvhp_llama_generate(void* model, int n_steps, int use_graph, int32_t* tokens_out,
+                        float* elapsed_ms);
+/* Device pointer and element count of a model tensor (fp16). */
+int kvhp_llama_tensor(void* model, int layer, int which, void** ptr, size_t* count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -93,6 +93,14 @@ _SIGNATURES = {
     "kvhp_argmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
     "kvhp_randn_f16": (_i32, [_vp, _i64, _u64, _u64, _f32, _vp]),
     "kvhp_fill_f16": (_i32, [_vp, _i64, _f32, _vp]),
+    # model runner
+    "kvhp_llama_create": (_i32, [_vp, _u64, _i32, ctypes.POINTER(ctypes.c_void_p)]),
+    "kvhp_llama_destroy": (_i32, [_vp]),
+    "kvhp_llama_prefill": (_i32, [_vp, _vp, _i32, _vp, _vp]),
+    "kvhp_llama_decode_step": (_i32, [_vp, ctypes.c_int32, _vp, _vp]),
+    "kvhp_llama_generate": (_i32, [_vp, _i32, _i32, _vp, _vp]),
+    "kvhp_llama_tensor": (_i32, [_vp, _i32, _i32, ctypes.POINTER(ctypes.c_void_p),
+                                 ctypes.POINTER(ctypes.c_size_t)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -311,3 +319,91 @@ def randn_f16(out, seed, stream_id, std, stream=None):
 
 def fill_f16(out, value, stream=None):
     _check(load().kvhp_fill_f16(_ptr(out), out.numel(), value, _stream(stream)))
+
+
+# ------------------------------------------------------------ model runner --
+class LlamaConfig(ctypes.Structure):
+    """kvhp_llama_config."""
+
+    _fields_ = [("vocab_size", ctypes.c_int), ("hidden_size", ctypes.c_int),
+                ("num_layers", ctypes.c_int), ("num_q_heads", ctypes.c_int),
+                ("num_kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+                ("ffn_size", ctypes.c_int), ("rms_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float), ("reserved", ctypes.c_int)]
+
+
+def llama_1b_config() -> LlamaConfig:
+    """22 layers, hidden 2048, 32 q / 4 KV heads of 64,
+    SwiGLU 5632, vocab 32000, RMSNorm eps 1e-5, RoPE theta 10000."""
+    return LlamaConfig(32000, 2048, 22, 32, 4, 64, 5632, 1e-5, 10000.0, 0)
+
+
+LLAMA_EMBED, LLAMA_LM_HEAD, LLAMA_FINAL_NORM = 0, 1, 2
+LLAMA_ATTN_NORM, LLAMA_FFN_NORM, LLAMA_W_QKV, LLAMA_W_O = 10, 11, 12, 13
+LLAMA_W_GATE_UP, LLAMA_W_DOWN, LLAMA_POOL_K, LLAMA_POOL_V = 14, 15, 16, 17
+
+
+class LlamaModel:
+    """The C ABI model runner: prefill_gpu / decode_step_gpu / on-device
+    greedy generation (host buffers are numpy arrays)."""
+
+    def __init__(self, config: LlamaConfig, seed: int, max_ctx: int):
+        import numpy as np
+        self._np = np
+        self.config = config
+        self.max_ctx = max_ctx
+        h = ctypes.c_void_p()
+        _check(load().kvhp_llama_create(ctypes.byref(config), seed, max_ctx, ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            load().kvhp_llama_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prefill(self, tokens):
+        np = self._np
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.config.vocab_size, np.float32)
+        nxt = ctypes.c_int32()
+        _check(load().kvhp_llama_prefill(self._h, t.ctypes.data, t.size, logits.ctypes.data,
+                                         ctypes.byref(nxt)))
+        return int(nxt.value), logits
+
+    def decode_step(self, token: int = -1):
+        np = self._np
+        logits = np.empty(self.config.vocab_size, np.float32)
+        nxt = ctypes.c_int32()
+        _check(load().kvhp_llama_decode_step(self._h, token, logits.ctypes.data,
+                                             ctypes.byref(nxt)))
+        return int(nxt.value), logits
+
+    def generate(self, n_steps: int, use_graph: bool = True):
+        """Returns (tokens since the prefill, device milliseconds of the steps)."""
+        np = self._np
+        out = np.zeros(self.max_ctx + 1, np.int32)
+        ms = ctypes.c_float()
+        _check(load().kvhp_llama_generate(self._h, n_steps, int(use_graph), out.ctypes.data,
+                                          ctypes.byref(ms)))
+        return out, float(ms.value)
+
+    def tensor(self, layer: int, which: int):
+        """Host copy (numpy float16) of a model tensor."""
+        np = self._np
+        ptr = ctypes.c_void_p()
+        n = ctypes.c_size_t()
+        _check(load().kvhp_llama_tensor(self._h, layer, which, ctypes.byref(ptr), ctypes.byref(n)))
+        out = np.empty(n.value, np.float16)
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipMemcpy.argtypes = [_vp, _vp, _sz, _i32]
+        hip.hipMemcpy.restype = _i32
+        rc = hip.hipMemcpy(out.ctypes.data, ptr.value, n.value * 2, 2)  # device to host
+        if rc != 0:
+            raise KVHPError(KVHP_ERR_HIP, f"hipMemcpy device-to-host failed ({rc})")
+        return out
