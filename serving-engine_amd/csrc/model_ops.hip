@@ -83,28 +83,6 @@ __device__ __forceinline__ void rope_cs(int pos, int i, int D, float theta, floa
 template <int KC, int RW, int EPI, bool RMS>
 __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
     const int lane = threadIdx.x;
-    half8 xr[KC];
-#pragma unroll
-    for (int j = 0; j < KC; ++j) xr[j] = load_half8(a.x + 512 * j + 8 * lane);
-    if constexpr (RMS) {
-        float ss = 0.f;
-#pragma unroll
-        for (int j = 0; j < KC; ++j)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float v = static_cast<float>(xr[j][e]);
-                ss = fmaf(v, v, ss);
-            }
-        ss = wave_sum_fast(ss);
-        const float rs = 1.f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
-#pragma unroll
-        for (int j = 0; j < KC; ++j) {
-            const half8 w = load_half8(a.norm_w + 512 * j + 8 * lane);
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                xr[j][e] = static_cast<f16>(static_cast<float>(xr[j][e]) * rs * static_cast<float>(w[e]));
-        }
-    }
 
     // The rows of this wave.
     int row[RW];
@@ -135,13 +113,57 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
         }
     }
 
-    float acc[RW];
+    // Weights, x and the norm weights are independent: every load is issued
+    // before the first use, so the wave makes one memory round trip (the
+    // scheduler would otherwise interleave loads and products to save
+    // registers, and the RMSNorm would serialise two more trips).
     half8 wr[RW][KC];
 #pragma unroll
     for (int i = 0; i < RW; ++i)
 #pragma unroll
         for (int j = 0; j < KC; ++j)
             wr[i][j] = load_half8_stream(a.W + (int64_t)row[i] * a.K + 512 * j + 8 * lane);
+    half8 xr[KC], nw[KC];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+        xr[j] = load_half8(a.x + 512 * j + 8 * lane);
+        if constexpr (RMS) nw[j] = load_half8(a.norm_w + 512 * j + 8 * lane);
+    }
+    // The epilogue's own reads (residual row, write position and its page)
+    // ride the same round trip.
+    float rv = 0.f;
+    if constexpr (EPI == kEpiResidual) {
+        int rr = row[0];
+#pragma unroll
+        for (int i = 1; i < RW; ++i)
+            if (lane == i) rr = row[i];
+        rv = static_cast<float>(a.resid[rr]);
+    }
+    int pos = 0, pid = -1;
+    if constexpr (EPI == kEpiQKV) {
+        pos = a.seq_len[0] - 1;
+        if (pos >= 0 && (pos >> 4) < a.max_pages) pid = a.bt[pos >> 4];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (RMS) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = static_cast<float>(xr[j][e]);
+                ss = fmaf(v, v, ss);
+            }
+        ss = wave_sum_fast(ss);
+        const float rs = 1.f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                xr[j][e] = static_cast<f16>(static_cast<float>(xr[j][e]) * rs *
+                                            static_cast<float>(nw[j][e]));
+    }
+    float acc[RW];
 #pragma unroll
     for (int i = 0; i < RW; ++i) {
         acc[i] = 0.f;
@@ -164,11 +186,8 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
         const int hh = wv / wph, pb = wv % wph;
         const int d = 4 * pb + lane;          // pair (d, d + D/2)
         const int half = a.D / 2;
-        const int pos = a.seq_len[0] - 1;
         if (hh >= a.Hq + a.Hkv) {             // v: no rotation
             const int kvh = hh - a.Hq - a.Hkv;
-            if (pos < 0 || (pos >> 4) >= a.max_pages) return;
-            const int pid = a.bt[pos >> 4];
             if (pid < 0 || pid >= a.num_pages) return;
             f16* dst = a.pool_v + (((int64_t)kvh * a.num_pages + pid) * kPage + (pos & 15)) * a.D;
             dst[d] = static_cast<f16>(x1);
@@ -184,8 +203,6 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
             a.y16[hh * a.D + d + half] = o2;
         } else {
             const int kvh = hh - a.Hq;
-            if (pos < 0 || (pos >> 4) >= a.max_pages) return;
-            const int pid = a.bt[pos >> 4];
             if (pid < 0 || pid >= a.num_pages) return;
             f16* dst = a.pool_k + (((int64_t)kvh * a.num_pages + pid) * kPage + (pos & 15)) * a.D;
             dst[d] = o1;
@@ -221,7 +238,7 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
         if constexpr (EPI == kEpiF32) {
             a.y32[n] = v;
         } else if constexpr (EPI == kEpiResidual) {
-            a.y16[n] = static_cast<f16>(v + static_cast<float>(a.resid[n]));
+            a.y16[n] = static_cast<f16>(v + rv);
         } else {
             a.y16[n] = static_cast<f16>(v);
         }
@@ -436,13 +453,30 @@ argmax_kernel(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, 
     __shared__ int64_t bi[16];
     float best = -INFINITY;
     int64_t idx = n;  // sentinel: larger than any index
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = logits[i];
+    auto take = [&](float v, int64_t i) {
         if (v > best || (idx == n && !(v != v))) {  // first non-NaN, then strictly greater
             best = v;
             idx = i;
         }
+    };
+    // Thread t scans float4 groups t, t + 1024, ... in ascending order (all
+    // of a pass's loads in flight), then the scalar tail.
+    const int64_t n4 = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 ? n / 4 : 0;
+    const floatx4* l4 = reinterpret_cast<const floatx4*>(logits);
+    constexpr int U = 8;
+    for (int64_t g0 = threadIdx.x; g0 < n4; g0 += (int64_t)U * blockDim.x) {
+        floatx4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t g = g0 + (int64_t)u * blockDim.x;
+            v[u] = g < n4 ? l4[g] : floatx4{NAN, NAN, NAN, NAN};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) take(v[u][e], 4 * (g0 + (int64_t)u * blockDim.x) + e);
     }
+    for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += blockDim.x) take(logits[i], i);
     // wave reduction: larger value wins, equal values -> smaller index
     for (int off = 32; off >= 1; off >>= 1) {
         const float ov = __shfl_xor(best, off);
