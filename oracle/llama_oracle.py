@@ -82,3 +82,55 @@ def top2_margin(logits):
     docs/GATES.md)."""
     two = np.partition(logits, -2)[-2:]
     return float(two.max() - two.min())
+
+
+# ---------------------------------------------------------------------------
+# The reference's own CPU model forward (src/model/forward_cpu.cpp, compiled
+# where it lies by `make -C oracle ref` into _ref/libref_forward.so), used by
+# tests to pin LlamaOracle's composition.  Absent where the reference tree is.
+import ctypes  # noqa: E402
+import os  # noqa: E402
+
+REF_FORWARD_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_ref",
+                               "libref_forward.so")
+_ref_fwd = None
+
+
+def ref_forward_available():
+    return os.path.exists(REF_FORWARD_LIB)
+
+
+def ref_flat_weights(weights, cfg):
+    """Pack LlamaOracle weights in ref_forward_shim.cpp's order: embed,
+    final_norm, then per layer input/post-attention norms, q, k, v, o, gate,
+    up, down (fused q|k|v and gate|up split back into their parts)."""
+    hq, hkv, d, f = cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, cfg.ffn_size
+    parts = [weights["embed"], weights["final_norm"]]
+    for lw in weights["layers"]:
+        qkv = lw["w_qkv"]
+        parts += [lw["attn_norm"], lw["ffn_norm"], qkv[:hq * d], qkv[hq * d:(hq + hkv) * d],
+                  qkv[(hq + hkv) * d:], lw["w_o"], lw["w_gate_up"][:f], lw["w_gate_up"][f:],
+                  lw["w_down"]]
+    return np.ascontiguousarray(np.concatenate([np.ravel(p) for p in parts]), np.float32)
+
+
+def ref_forward_cpu(ids, cfg, weights):
+    """Logits [S][V] of the reference forward over `ids` (biases zero, LM
+    head = embedding, as the reference ties them)."""
+    global _ref_fwd
+    if _ref_fwd is None:
+        lib = ctypes.CDLL(REF_FORWARD_LIB)
+        f = lib.ref_forward_cpu
+        f.restype = ctypes.c_int
+        f.argtypes = [np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS"), ctypes.c_int64] + \
+            [ctypes.c_int] * 7 + [ctypes.c_float] * 2 + \
+            [np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")] * 2
+        _ref_fwd = f
+    ids = np.ascontiguousarray(ids, np.int64)
+    out = np.zeros((ids.size, cfg.vocab_size), np.float32)
+    rc = _ref_fwd(ids, ids.size, cfg.vocab_size, cfg.hidden_size, cfg.ffn_size, cfg.num_layers,
+                  cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, cfg.rms_eps, cfg.rope_theta,
+                  ref_flat_weights(weights, cfg), out)
+    if rc != 0:
+        raise ValueError("ref_forward_cpu: num_q_heads * head_dim must equal hidden_size")
+    return out
