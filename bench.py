@@ -53,10 +53,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5")
     ap.add_argument("--profile", nargs="?", const="decode", default=None,
-                    choices=("decode", "prefill"),
+                    choices=("decode", "prefill", "c5"),
                     help="short run for rocprofv3: a 256 MiB device copy (counter "
-                         "calibration) then the config-3 steps (decode) or config-4 "
-                         "S=2048 prefill calls (prefill); no CPU baseline, no extras")
+                         "calibration) then the config-3 steps (decode), config-4 "
+                         "S=2048 prefill calls (prefill) or --steps config-5 decode "
+                         "steps without the HIP graph (c5); no CPU baseline, no extras")
     return ap.parse_args()
 
 
@@ -353,6 +354,19 @@ def run_config5(torch, kvhp, steps=128, prompt_len=2048):
             "first_tokens": toks[:8].tolist()}
 
 
+def run_config5_eager(torch, kvhp, steps=32, prompt_len=2048):
+    """Config 5 decode steps launched kernel by kernel (no HIP graph), so a
+    kernel trace sees every launch of the step (profiling mode)."""
+    cfg = kvhp.llama_1b_config()
+    model = kvhp.LlamaModel(cfg, seed=5, max_ctx=prompt_len + steps + 1)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, prompt_len).astype(np.int32)
+    model.prefill(prompt)
+    toks, ms = model.generate(steps, use_graph=False)
+    model.close()
+    return {"steps": steps, "ms_per_token_no_graph": round(ms / steps, 4),
+            "first_tokens": toks[:8].tolist()}
+
+
 def traffic_from_profile(dbytes):
     """HBM bytes per decode call from the committed rocprofv3 --pmc summary
     (profiles/decode_config3_traffic.json), if present."""
@@ -391,6 +405,10 @@ def main():
         if args.profile == "prefill":
             r4 = run_config4(torch, kvhp, sizes=(2048,), reps=args.steps)
             print(json.dumps({"profile": "prefill", "config4": r4}))
+            return
+        if args.profile == "c5":
+            r5 = run_config5_eager(torch, kvhp, steps=args.steps)
+            print(json.dumps({"profile": "c5", "config5": r5}))
             return
     log("config3 timed steps ...")
     r = run_config3(torch, kvhp, args)

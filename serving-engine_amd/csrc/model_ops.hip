@@ -34,7 +34,6 @@ namespace kvhp {
 
 namespace {
 
-typedef f16 half2v __attribute__((ext_vector_type(2)));
 
 enum Epilogue : int { kEpiF16 = 0, kEpiResidual = 1, kEpiF32 = 2, kEpiSwiglu = 3, kEpiQKV = 4 };
 

@@ -357,16 +357,21 @@ prefill_mfma_kernel(const PrefillArgs a) {
             }
             const float nmc = -m_run * a.scale_log2;
             half8 pop[2 * NKB];
-            float ls = 0.f;
 #pragma unroll
             for (int t = 0; t < 2 * NKB; ++t)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float p = fast_exp2(fmaf(scur[t / 2][8 * (t % 2) + e], a.scale_log2, nmc));
-                    pop[t][e] = static_cast<f16>(p);
-                    ls += p;
-                }
-            l_part += ls;
+                for (int e = 0; e < 8; ++e)
+                    pop[t][e] = static_cast<f16>(
+                        fast_exp2(fmaf(scur[t / 2][8 * (t % 2) + e], a.scale_log2, nmc)));
+            // Row sum of the fp16 P actually fed to the PV contraction, two
+            // values per v_dot2_f32_f16 with fp32 accumulation.
+            const half2v ones = {static_cast<f16>(1.f), static_cast<f16>(1.f)};
+#pragma unroll
+            for (int t = 0; t < 2 * NKB; ++t)
+#pragma unroll
+                for (int e = 0; e < 8; e += 2)
+                    l_part = __builtin_amdgcn_fdot2(half2v{pop[t][e], pop[t][e + 1]}, ones, l_part,
+                                                    false);
 
             // ---- O^T += V^T P^T: lane j16 of 16-lane block (h, blk2) reads
             //      rows R(j16/4) at dims 32db + 16*blk2 + 4*(j16%4).
