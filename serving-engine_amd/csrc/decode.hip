@@ -10,8 +10,8 @@
 // Per 32-token step (2 pages of 16 tokens), both contractions run on
 // v_mfma_f32_16x16x32_f16 in transposed form, so that lane (g, col) owns
 // query head `col` for the whole online softmax:
-//   S^T = K Q^T     A = K rows loaded straight from HBM (lane: token col of
-//                   a page, 16 B at dims 32c + 8g), B = Q^T held in
+//   S^T = K Q^T     A = K rows from the LDS tile (lane: token col of a
+//                   page, 16 B at dims 32c + 8g), B = Q^T held in
 //                   registers (zero columns for heads >= G).
 //   softmax         fp32 in the log2 domain; per-lane max over its 8 tokens,
 //                   then v_permlane16/32_swap across the four lane rows (no
@@ -20,10 +20,13 @@
 //   O^T += V^T P^T  A = V^T read from a padded LDS tile with
 //                   ds_read_b64_tr_b16 (transposing 8-byte reads), B = P^T in
 //                   fp16 straight from the S^T accumulators.
-// K is fetched two steps ahead into registers and V one step ahead (V goes
-// through LDS for the transposed reads), with non-temporal loads (the cache
-// is streamed once) and identical loads on every path so the compiler keeps
-// exact vmcnt waits.  246 VGPRs at D=128: two waves per SIMD.
+// K is fetched two steps ahead into registers and V one step ahead, both as
+// whole rows per load (contiguous bytes; loading K straight in the MFMA
+// layout, 64 bytes of each of 16 rows per load, cost ~5 % of HBM
+// throughput), then staged through LDS: K back in the A layout, V for the
+// transposed reads.  Non-temporal loads (the cache is streamed once) and
+// identical loads on every path so the compiler keeps exact vmcnt waits.
+// 252 VGPRs and 17.9 KB LDS at D=128: two waves per SIMD, eight per CU.
 //
 // Splits: a sequence whose keys fit one split gets its output written
 // directly; otherwise each split stores (m, l, o[D]) in fp32 and
@@ -94,8 +97,8 @@ __device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
 // One 64-lane workgroup per (split, kv_head, sequence).  Both contractions
 // are transposed so that lane (g, col) -- g = lane/16, col = lane%16 -- owns
 // query head `col` of the KV head's group for the whole online softmax:
-//   S^T = K Q^T   A = K rows of one 16-token page (lane: token col, dims
-//                 32c+8g..+8, 64 contiguous bytes per row), B = Q^T (lane:
+//   S^T = K Q^T   A = K rows of one 16-token page from k_lds (lane: token
+//                 col, dims 32c+8g..+8), B = Q^T (lane:
 //                 head col, same dims; zero for col >= G).  Lane (g, col)
 //                 gets tokens 4g+e of the page for head col.
 //   softmax       per head = per lane: in-lane max over its 8 tokens of the
@@ -104,8 +107,9 @@ __device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
 //                 16db+col, tokens 4g..4g+3 and 16+4g..16+4g+3), B = P^T in
 //                 fp16 straight from the S^T accumulators (k-slot (g, e) is
 //                 token 4g+e of page 0 for e < 4, of page 1 for e >= 4).
-// K runs two steps ahead in registers, V one step (it is staged through LDS
-// for the transposed reads).
+// K runs two steps ahead in registers, V one step; both are loaded as whole
+// rows and staged through LDS (K for the A layout, V for the transposed
+// reads).
 template <int D, int G, bool PAGED>
 __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_splitk_kernel(const DecodeArgs a) {
@@ -115,10 +119,12 @@ decode_splitk_kernel(const DecodeArgs a) {
     constexpr int ND = D / 16;       // 16-dim output blocks
     constexpr int LPR = D / 8;       // lanes per V row (16 B each)
     constexpr int RPL = kWave / LPR; // V rows per wave load
-    constexpr int NVL = TOK / RPL;   // V loads per step
+    constexpr int NVL = TOK / RPL;   // V (and K) loads per step
     constexpr int VP = D + 16;       // V tile row pitch in halfs (bank skew)
+    constexpr int KP = D + 8;        // K tile row pitch in halfs (bank skew)
 
     __shared__ __attribute__((aligned(16))) f16 v_lds[TOK * VP];
+    __shared__ __attribute__((aligned(16))) f16 k_lds[TOK * KP];
 
     const int lane = threadIdx.x;
     const int g = lane >> 4;
@@ -204,21 +210,27 @@ decode_splitk_kernel(const DecodeArgs a) {
         return reinterpret_cast<const char*>(base + row * ss);
     };
 
-    half8 kbuf[2][2][NC];  // [ring slot][page][k-chunk]
+    half8 kbuf[2][NVL];    // [ring slot][load]: whole rows, as V
     half8 vbuf[NVL];
     const uint32_t kss = static_cast<uint32_t>(ssk) * 2u;  // row pitch, bytes
     const uint32_t vss = static_cast<uint32_t>(ssv) * 2u;
 
+    // K and V are fetched the same way: lane (vrow, vdim) loads 16 bytes of
+    // row RPL*j + vrow, so each load covers RPL whole rows (contiguous
+    // bytes; the MFMA layout, 64 bytes of 16 rows per load, cost ~5 % of HBM
+    // throughput).  K reaches its operand layout through k_lds.
     auto load_k = [&](auto S_, int T0) {
         constexpr int S = decltype(S_)::value;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             int lim;
             const char* pb = page_base(kbase, ssk, T0, t, lim);
-            const uint32_t off = __umul24(static_cast<uint32_t>(min(col, lim)), kss) + 16u * g;
 #pragma unroll
-            for (int c = 0; c < NC; ++c)
-                kbuf[S][t][c] = load_half8_stream(reinterpret_cast<const f16*>(pb + off + 64 * c));
+            for (int j = t * (kPage / RPL); j < (t + 1) * (kPage / RPL); ++j) {
+                const int s0 = ((RPL * j) & (kPage - 1)) + vrow;
+                const uint32_t off = __umul24(static_cast<uint32_t>(min(s0, lim)), kss) + 2u * vdim;
+                kbuf[S][j] = load_half8_stream(reinterpret_cast<const f16*>(pb + off));
+            }
         }
     };
     auto load_v = [&](int T0) {
@@ -249,16 +261,22 @@ decode_splitk_kernel(const DecodeArgs a) {
         constexpr bool PFV = decltype(PFV_)::value;
         const int T0 = t_begin + TOK * it;
 
-        // ---- S^T = K Q^T for the two pages of the step.
+        // ---- S^T = K Q^T for the two pages of the step: K rows into LDS,
+        //      back in the A layout (lane (g, col): token col, dims 32c+8g).
+#pragma unroll
+        for (int j = 0; j < NVL; ++j)
+            *reinterpret_cast<half8*>(&k_lds[(RPL * j + vrow) * KP + vdim]) = kbuf[S][j];
+        if constexpr (PFK) load_k(S_, T0 + 2 * TOK);
         floatx4 C[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             C[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < NC; ++c)
-                C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbuf[S][t][c], qb[c], C[t], 0, 0, 0);
+            for (int c = 0; c < NC; ++c) {
+                const half8 ka = *reinterpret_cast<const half8*>(&k_lds[(16 * t + col) * KP + 32 * c + 8 * g]);
+                C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[c], C[t], 0, 0, 0);
+            }
         }
-        if constexpr (PFK) load_k(S_, T0 + 2 * TOK);
 
         // ---- tokens past the split (only in its last step).
         if (T0 + TOK > t_end) {
