@@ -380,10 +380,11 @@ decode_splitk_kernel(const DecodeArgs a) {
 }
 
 // Log-sum-exp merge of the split partials of one (kv_head, sequence), four
-// waves per workgroup: all threads stage (m, l) of every (head, split) in
-// LDS; wave w turns heads w, w+4, ... into merge weights; then wave w sums
-// splits w, w+4, ... of every (head, 8-dim group) with all its loads in
-// flight at once, and the four partial sums are added through LDS.
+// waves per workgroup, one memory round trip: lane (head h, 8 dims) of wave w
+// folds splits w, w+4, w+8, ... into a running (max M, sum S, weighted o)
+// with the (m, l) and o loads of U splits in flight at once; the four wave
+// states then meet in LDS.  Partials hold o unnormalised and its sum l
+// relative to the split's own max m (log2 units).
 constexpr int kMergeWaves = 4;
 
 template <int D, int G>
@@ -392,10 +393,9 @@ decode_merge_kernel(const DecodeArgs a) {
     constexpr int LPR = D / 8;          // lanes per head row (8 dims each)
     constexpr int HPP = kWave / LPR;    // heads per pass of one wave
     constexpr int NP = (G + HPP - 1) / HPP;
-    constexpr int U = 8;                // splits in flight per lane
-    __shared__ float w_lds[G][kMaxSplits];
-    __shared__ float l_lds[G][kMaxSplits];
-    __shared__ __attribute__((aligned(16))) float red[kMergeWaves - 1][NP * HPP][D];
+    constexpr int U = 4;                // splits in flight per lane
+    __shared__ __attribute__((aligned(16))) float red_o[kMergeWaves - 1][NP][kWave][8];
+    __shared__ float red_ms[kMergeWaves - 1][NP][kWave][2];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -409,53 +409,48 @@ decode_merge_kernel(const DecodeArgs a) {
     const int nsb = (L + a.chunk - 1) / a.chunk;
     if (nsb <= 1) return;  // written directly by the split kernel
 
-    for (int i = tid; i < G * nsb; i += kMergeWaves * kWave) {
-        const int h = i / nsb, j = i - h * nsb;
-        const float2 v = *reinterpret_cast<const float2*>(a.ws_ml + ((row0 + h) * a.nsplit + j) * 2);
-        w_lds[h][j] = v.x;
-        l_lds[h][j] = v.y;
-    }
-    __syncthreads();
-    for (int h = wave; h < G; h += kMergeWaves) {
-        float mx = -INFINITY;
-        for (int j = lane; j < nsb; j += kWave) mx = fmaxf(mx, w_lds[h][j]);
-        mx = wave_max(mx);
-        float ls = 0.f;
-        for (int j = lane; j < nsb; j += kWave) ls += l_lds[h][j] * fast_exp2(w_lds[h][j] - mx);
-        ls = wave_sum(ls);
-        const float inv = ls > 0.f ? 1.f / ls : 0.f;
-        for (int j = lane; j < nsb; j += kWave) w_lds[h][j] = fast_exp2(w_lds[h][j] - mx) * inv;
-    }
-    __syncthreads();
-
+    float M[NP], Sm[NP];
     floatx4 acc[NP][2];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
+        M[p] = -3.0e38f;   // below every partial max; exp2 of the gap is 0
+        Sm[p] = 0.f;
         acc[p][0] = floatx4{0.f, 0.f, 0.f, 0.f};
         acc[p][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-        const int h = p * HPP + lane / LPR;
-        if (h >= G) continue;
-        const float* po = a.ws_o + (row0 + h) * a.nsplit * D + 8 * (lane % LPR);
+        const int h = min(p * HPP + lane / LPR, G - 1);
+        const int64_t prow = (row0 + h) * a.nsplit;
+        const float* po = a.ws_o + prow * D + 8 * (lane % LPR);
+        const float* pml = a.ws_ml + prow * 2;
         for (int j0 = wave; j0 < nsb; j0 += kMergeWaves * U) {
+            float2 ml[U];
             floatx4 x[U][2];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int j = min(j0 + kMergeWaves * u, nsb - 1);
+                ml[u] = *reinterpret_cast<const float2*>(pml + 2 * j);
                 x[u][0] = *reinterpret_cast<const floatx4*>(po + (int64_t)j * D);
                 x[u][1] = *reinterpret_cast<const floatx4*>(po + (int64_t)j * D + 4);
             }
+            __builtin_amdgcn_sched_barrier(0);  // all U splits' loads in flight first
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int j = j0 + kMergeWaves * u;
-                const float w = j < nsb ? w_lds[h][j] : 0.f;
-                acc[p][0] += w * x[u][0];
-                acc[p][1] += w * x[u][1];
+                // splits past the end (clamped re-loads) get weight 0
+                const float mu = j0 + kMergeWaves * u < nsb ? ml[u].x : -3.0e38f;
+                const float mn = fmaxf(M[p], mu);
+                const float al = fast_exp2(M[p] - mn);
+                const float be = fast_exp2(mu - mn);
+                acc[p][0] = acc[p][0] * al + x[u][0] * be;
+                acc[p][1] = acc[p][1] * al + x[u][1] * be;
+                Sm[p] = fmaf(Sm[p], al, ml[u].y * be);
+                M[p] = mn;
             }
         }
         if (wave > 0) {
-            float* r = &red[wave - 1][p * HPP + lane / LPR][8 * (lane % LPR)];
+            float* r = red_o[wave - 1][p][lane];
             *reinterpret_cast<floatx4*>(r) = acc[p][0];
             *reinterpret_cast<floatx4*>(r + 4) = acc[p][1];
+            red_ms[wave - 1][p][lane][0] = M[p];
+            red_ms[wave - 1][p][lane][1] = Sm[p];
         }
     }
     __syncthreads();
@@ -463,18 +458,25 @@ decode_merge_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
         const int h = p * HPP + lane / LPR;
-        if (h >= G) continue;
 #pragma unroll
         for (int w = 0; w < kMergeWaves - 1; ++w) {
-            const float* r = &red[w][p * HPP + lane / LPR][8 * (lane % LPR)];
-            acc[p][0] += *reinterpret_cast<const floatx4*>(r);
-            acc[p][1] += *reinterpret_cast<const floatx4*>(r + 4);
+            const float mw = red_ms[w][p][lane][0];
+            const float mn = fmaxf(M[p], mw);
+            const float al = fast_exp2(M[p] - mn);
+            const float be = fast_exp2(mw - mn);
+            const float* r = red_o[w][p][lane];
+            acc[p][0] = acc[p][0] * al + *reinterpret_cast<const floatx4*>(r) * be;
+            acc[p][1] = acc[p][1] * al + *reinterpret_cast<const floatx4*>(r + 4) * be;
+            Sm[p] = fmaf(Sm[p], al, red_ms[w][p][lane][1] * be);
+            M[p] = mn;
         }
+        if (h >= G) continue;
+        const float inv = Sm[p] > 0.f ? 1.f / Sm[p] : 0.f;
         half8 hv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            hv[e] = static_cast<f16>(acc[p][0][e]);
-            hv[4 + e] = static_cast<f16>(acc[p][1][e]);
+            hv[e] = static_cast<f16>(acc[p][0][e] * inv);
+            hv[4 + e] = static_cast<f16>(acc[p][1][e] * inv);
         }
         store_half8(a.out + (row0 + h) * D + 8 * (lane % LPR), hv);
     }
