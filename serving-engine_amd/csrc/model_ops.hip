@@ -139,11 +139,21 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
         rv = static_cast<float>(a.resid[rr]);
     }
     int pos = 0, pid = -1;
+    float rc = 1.f, rs = 0.f;  // RoPE rotation of this lane's pair
     if constexpr (EPI == kEpiQKV) {
         pos = a.seq_len[0] - 1;
         if (pos >= 0 && (pos >> 4) < a.max_pages) pid = a.bt[pos >> 4];
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (EPI == kEpiQKV) {
+        // The angle depends only on the position and the pair: computed here,
+        // under the weight loads, instead of after the products.
+        const int hh = wv / (a.D / 8);
+        if (hh < a.Hq + a.Hkv) {
+            rope_cs(pos < 0 ? 0 : pos, 4 * (wv % (a.D / 8)) + lane, a.D, a.theta, rc, rs);
+            asm volatile("" ::"v"(rc), "v"(rs));
+        }
+    }
     if constexpr (RMS) {
         float ss = 0.f;
 #pragma unroll
@@ -193,8 +203,7 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
             dst[d + half] = static_cast<f16>(x2);
             return;
         }
-        float c, s;
-        rope_cs(pos < 0 ? 0 : pos, d, a.D, a.theta, c, s);
+        const float c = rc, s = rs;
         const f16 o1 = static_cast<f16>(x1 * c - x2 * s);
         const f16 o2 = static_cast<f16>(x2 * c + x1 * s);
         if (hh < a.Hq) {
