@@ -34,6 +34,12 @@ int fail(int code, const char* fmt, ...);
 // Report the launch status of the kernels just enqueued.
 int check_launch(const char* what);
 
+// kvhp_argmax that also copies row `token` of embed [V][hidden] into x
+// (model_ops.hip; used by the model runner so that a decode step starts
+// from x without an embedding launch).
+int argmax_embed(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, int32_t* log,
+                 int32_t* log_count, const void* embed, int64_t hidden, void* x, hipStream_t s);
+
 #define KVHP_REQUIRE(cond, code, ...)          \
     do {                                       \
         if (!(cond)) return ::kvhp::fail(code, __VA_ARGS__); \

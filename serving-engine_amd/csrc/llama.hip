@@ -139,11 +139,15 @@ kvhp_kv_view pool_view(const Model& m, const f16* pool) {
 }
 
 // One decode step on the device: token m.state[1] at position m.state[0] - 1.
-int decode_step_kernels(Model& m) {
+// The greedy argmax that ends the prefill and every step also writes the
+// chosen token's embedding row into m.x, so a step that continues from it
+// starts without an embedding launch; embed_token re-reads m.state[1]
+// (after the caller replaced the token).
+int decode_step_kernels(Model& m, bool embed_token) {
     const kvhp_llama_config& c = m.c;
     const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
     void* s = m.stream;
-    KVHP_TRY(kvhp_embedding(m.state + 1, m.embed, m.x, 1, H, c.vocab_size, s));
+    if (embed_token) KVHP_TRY(kvhp_embedding(m.state + 1, m.embed, m.x, 1, H, c.vocab_size, s));
     for (const Layer& L : m.layers) {
         KVHP_TRY(kvhp_rmsnorm_qkv_rope_append(L.w_qkv, m.x, L.attn_norm, c.rms_eps, m.state,
                                               c.rope_theta, m.q1, L.pool_k, L.pool_v, m.bt, m.P,
@@ -158,7 +162,8 @@ int decode_step_kernels(Model& m) {
     }
     KVHP_TRY(kvhp_rmsnorm_gemv(m.lm_head, m.x, m.final_norm, c.rms_eps, nullptr, m.logits,
                                c.vocab_size, H, s));
-    return kvhp_argmax(m.logits, c.vocab_size, m.state + 1, m.state, m.log, m.state + 2, s);
+    return argmax_embed(m.logits, c.vocab_size, m.state + 1, m.state, m.log, m.state + 2, m.embed,
+                        H, m.x, static_cast<hipStream_t>(s));
 }
 
 }  // namespace
@@ -291,7 +296,8 @@ extern "C" int kvhp_llama_prefill(void* model, const int32_t* tokens, int n, flo
              "hipMemcpyAsync(last row)");
     KVHP_TRY(kvhp_rmsnorm_gemv(m.lm_head, m.x, m.final_norm, c.rms_eps, nullptr, m.logits,
                                c.vocab_size, H, s));
-    KVHP_TRY(kvhp_argmax(m.logits, c.vocab_size, m.state + 1, m.state, m.log, m.state + 2, s));
+    KVHP_TRY(argmax_embed(m.logits, c.vocab_size, m.state + 1, m.state, m.log, m.state + 2,
+                          m.embed, H, m.x, static_cast<hipStream_t>(s)));
     if (logits_out)
         KVHP_HIP(hipMemcpyAsync(logits_out, m.logits, (size_t)c.vocab_size * 4,
                                 hipMemcpyDeviceToHost, m.stream),
@@ -321,7 +327,7 @@ extern "C" int kvhp_llama_decode_step(void* model, int32_t token, float* logits_
     if (token >= 0)  // teacher forcing: replace the greedy token of the last step
         KVHP_HIP(hipMemcpyAsync(m.state + 1, &token, 4, hipMemcpyHostToDevice, m.stream),
                  "hipMemcpyAsync(token)");
-    KVHP_TRY(decode_step_kernels(m));
+    KVHP_TRY(decode_step_kernels(m, token >= 0));
     if (logits_out)
         KVHP_HIP(hipMemcpyAsync(logits_out, m.logits, (size_t)m.c.vocab_size * 4,
                                 hipMemcpyDeviceToHost, m.stream),
@@ -349,7 +355,7 @@ extern "C" int kvhp_llama_generate(void* model, int n_steps, int use_graph, int3
     if (use_graph && !m.graph_exec) {
         KVHP_HIP(hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal),
                  "hipStreamBeginCapture");
-        const int rc = decode_step_kernels(m);
+        const int rc = decode_step_kernels(m, false);
         hipGraph_t g = nullptr;
         const hipError_t e = hipStreamEndCapture(m.stream, &g);
         if (rc) {
@@ -369,7 +375,7 @@ extern "C" int kvhp_llama_generate(void* model, int n_steps, int use_graph, int3
         if (use_graph)
             KVHP_HIP(hipGraphLaunch(m.graph_exec, m.stream), "hipGraphLaunch");
         else
-            KVHP_TRY(decode_step_kernels(m));
+            KVHP_TRY(decode_step_kernels(m, false));
     }
     KVHP_HIP(hipEventRecord(e1, m.stream), "hipEventRecord");
     KVHP_HIP(hipEventSynchronize(e1), "hipEventSynchronize");

@@ -452,23 +452,26 @@ __global__ void embedding_kernel(const int32_t* ids, const f16* table, f16* out,
 }
 
 // Greedy argmax of fp32 logits, lowest index on ties; NaN never wins.
-// Optionally appends the token to log[count] (count = *log_count, then
-// incremented) and advances *seq_len by one.
+// Each candidate is one 64-bit key, (order-preserving bits of the value) <<
+// 32 | ~index, so every reduction step is a single unsigned max: the larger
+// value wins, then the smaller index; NaN maps below -inf.  Optionally
+// appends the token to log[count] (count = *log_count, then incremented),
+// advances *seq_len by one, and copies the token's embedding row into x
+// (the next decode step's input, so that step needs no embedding launch).
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t ord = (v != v) ? 0u : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+    return (static_cast<uint64_t>(ord) << 32) | static_cast<uint64_t>(~i);
+}
+
 __global__ void __launch_bounds__(1024)
 argmax_kernel(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, int32_t* log,
-              int32_t* log_count) {
-    __shared__ float bv[16];
-    __shared__ int64_t bi[16];
-    float best = -INFINITY;
-    int64_t idx = n;  // sentinel: larger than any index
-    auto take = [&](float v, int64_t i) {
-        if (v > best || (idx == n && !(v != v))) {  // first non-NaN, then strictly greater
-            best = v;
-            idx = i;
-        }
-    };
-    // Thread t scans float4 groups t, t + 1024, ... in ascending order (all
-    // of a pass's loads in flight), then the scalar tail.
+              int32_t* log_count, const f16* embed, int64_t hidden, f16* x) {
+    __shared__ uint64_t red[16];
+    __shared__ int32_t tok_lds;
+    uint64_t best = 0;  // below every candidate (a NaN candidate has ~i > 0)
+    // Thread t scans float4 groups t, t + 1024, ... (all of a pass's loads
+    // in flight), then the scalar tail.
     const int64_t n4 = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 ? n / 4 : 0;
     const floatx4* l4 = reinterpret_cast<const floatx4*>(logits);
     constexpr int U = 8;
@@ -476,40 +479,58 @@ argmax_kernel(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, 
         floatx4 v[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            const int64_t g = min(g0 + (int64_t)u * blockDim.x, n4 - 1);
+            v[u] = l4[g];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
             const int64_t g = g0 + (int64_t)u * blockDim.x;
-            v[u] = g < n4 ? l4[g] : floatx4{NAN, NAN, NAN, NAN};
+            if (g < n4) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint64_t k = argmax_key(v[u][e], static_cast<uint32_t>(4 * g + e));
+                    best = k > best ? k : best;
+                }
+            }
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) take(v[u][e], 4 * (g0 + (int64_t)u * blockDim.x) + e);
     }
-    for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += blockDim.x) take(logits[i], i);
-    // wave reduction: larger value wins, equal values -> smaller index
+    for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += blockDim.x) {
+        const uint64_t k = argmax_key(logits[i], static_cast<uint32_t>(i));
+        best = k > best ? k : best;
+    }
     for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(best, off);
-        const int64_t oi = __shfl_xor(idx, off);
-        if (ov > best || (ov == best && oi < idx) || (idx == n && oi < n)) {
-            best = ov;
-            idx = oi;
-        }
+        const uint64_t o = __shfl_xor(best, off);
+        best = o > best ? o : best;
     }
     const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        bv[w] = best;
-        bi[w] = idx;
-    }
+    const int nw = static_cast<int>(blockDim.x >> 6);
+    if ((threadIdx.x & 63) == 0) red[w] = best;
     __syncthreads();
-    if (threadIdx.x != 0) return;
-    for (int i = 1; i < static_cast<int>(blockDim.x >> 6); ++i)
-        if (bv[i] > best || (bv[i] == best && bi[i] < idx) || (idx == n && bi[i] < n)) {
-            best = bv[i];
-            idx = bi[i];
+    if (threadIdx.x < 64) {
+        best = threadIdx.x < static_cast<unsigned>(nw) ? red[threadIdx.x] : 0;
+        for (int off = 32; off >= 1; off >>= 1) {
+            const uint64_t o = __shfl_xor(best, off);
+            best = o > best ? o : best;
         }
-    const int32_t tok = idx < n ? static_cast<int32_t>(idx) : 0;
-    *token = tok;
-    if (log) log[(*log_count)++] = tok;
-    if (seq_len) *seq_len += 1;
+        if (threadIdx.x == 0) {
+            const uint32_t idx = ~static_cast<uint32_t>(best);
+            const int32_t tok = best != 0 && idx < n ? static_cast<int32_t>(idx) : 0;
+            *token = tok;
+            tok_lds = tok;
+            if (log) log[(*log_count)++] = tok;
+            if (seq_len) *seq_len += 1;
+        }
+    }
+    if (embed == nullptr) return;
+    __syncthreads();
+    const f16* row = embed + static_cast<int64_t>(tok_lds) * hidden;
+    if ((hidden & 7) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        for (int64_t i = threadIdx.x; i < hidden / 8; i += blockDim.x)
+            store_half8(x + 8 * i, load_half8(row + 8 * i));
+    } else {
+        for (int64_t i = threadIdx.x; i < hidden; i += blockDim.x) x[i] = row[i];
+    }
 }
 
 // Seeded N(0, std) fill: element i of stream `stream_id` is a Box-Muller
@@ -747,9 +768,20 @@ extern "C" int kvhp_argmax(const float* logits, int64_t n, int32_t* token, int32
     KVHP_REQUIRE((log == nullptr) == (log_count == nullptr), KVHP_ERR_INVALID,
                  "argmax: log and log_count go together");
     hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
-                       logits, n, token, seq_len, log, log_count);
+                       logits, n, token, seq_len, log, log_count, nullptr, int64_t{0}, nullptr);
     return check_launch("argmax");
 }
+
+namespace kvhp {
+int argmax_embed(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, int32_t* log,
+                 int32_t* log_count, const void* embed, int64_t hidden, void* x, hipStream_t s) {
+    KVHP_REQUIRE(logits && token && embed && x && n > 0 && n < (int64_t)1 << 31 && hidden > 0,
+                 KVHP_ERR_INVALID, "argmax_embed: bad arguments");
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, n, token, seq_len, log,
+                       log_count, static_cast<const f16*>(embed), hidden, static_cast<f16*>(x));
+    return check_launch("argmax_embed");
+}
+}  // namespace kvhp
 
 extern "C" int kvhp_randn_f16(void* out, int64_t count, uint64_t seed, uint64_t stream_id,
                               float std_dev, void* stream) {

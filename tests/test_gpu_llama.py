@@ -93,6 +93,29 @@ def test_config5_graph_generation_matches_stepwise():
     b.close()
 
 
+def test_config5_teacher_forced_step_matches_continue():
+    """A step that continues from the last greedy token takes its input row
+    from the argmax (which copies the embedding into the hidden state); a
+    step given the same token explicitly runs the embedding kernel.  Both
+    must produce identical logits."""
+    cfg = kvhp.llama_1b_config()
+    prompt = np.random.default_rng(13).integers(0, cfg.vocab_size, 24).astype(np.int32)
+    a = kvhp.LlamaModel(cfg, seed=9, max_ctx=64)
+    t, _ = a.prefill(prompt)
+    cont = []
+    for _ in range(3):
+        t, lg = a.decode_step()
+        cont.append((t, lg))
+    a.close()
+    b = kvhp.LlamaModel(cfg, seed=9, max_ctx=64)
+    t, _ = b.prefill(prompt)
+    for i in range(3):
+        t, lg = b.decode_step(int(t))
+        assert t == cont[i][0]
+        assert np.array_equal(lg, cont[i][1]), f"step {i}: logits differ"
+    b.close()
+
+
 def test_llama_api_errors():
     cfg = kvhp.llama_1b_config()
     bad = kvhp.LlamaConfig(100, 96, 1, 3, 2, 32, 64, 1e-5, 1e4, 0)  # 3 q heads on 2 kv heads
