@@ -131,6 +131,25 @@ int kvhp_decode_attention(const void* q, const kvhp_kv_view* k_view,
                           int num_splits, void* workspace,
                           size_t workspace_bytes, void* stream);
 
+/* The serving step's append_kv_cache + decode_gqa_split pair
+ * (src/model/forward_gpu.cu:593-640: append the new K/V row at pos, then
+ * attend over pos+1 keys) in one call on paged views:
+ *   k_new / v_new [batch][Hkv][D] fp16 (one token per sequence), written to
+ *   position positions[b] (device int32[batch]) of the pools through the
+ *   views' block table, exactly as kvhp_paged_append_kv (same drop rules),
+ *   then attention as kvhp_decode_attention over seq_lens[b] keys, the new
+ *   row included when positions[b] < seq_lens[b].
+ * Within the fast kernel's shapes the row is attended from registers and
+ * written by the one workgroup that covers it (no separate append launch);
+ * otherwise the append kernel runs first.  Workspace as for
+ * kvhp_decode_attention. */
+int kvhp_paged_append_decode(const void* q, const void* k_new, const void* v_new,
+                             const kvhp_kv_view* k_view, const kvhp_kv_view* v_view,
+                             const int32_t* positions, const int32_t* seq_lens, void* out,
+                             int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                             int max_seq_len, int num_splits, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* Replaces engine::cuda::decode_gqa (src/cuda/kernels.h:104-115,
  * src/cuda/decode_attention.cu:114-137): one sequence, head-major cache
  * [Hkv][max_seq][D], total_seq_len keys; routed to kvhp_decode_attention. */

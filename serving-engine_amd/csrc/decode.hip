@@ -71,6 +71,14 @@ struct DecodeArgs {
     int cap;               // tokens addressable per sequence
     int fixed_len;         // length of every sequence when seq_lens == nullptr
     float scale_log2;      // log2(e) / sqrt(D)
+    // Fused append (paged only; k_new == nullptr: none): row b of k_new /
+    // v_new [B][Hkv][D] is the token at position new_pos[b]; the split that
+    // covers it writes it into its page before reading the page.
+    const f16* k_new;
+    const f16* v_new;
+    const int32_t* new_pos;
+    f16* pool_k;           // the K / V pools of the views, writable
+    f16* pool_v;
 };
 
 __device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
@@ -151,6 +159,33 @@ decode_splitk_kernel(const DecodeArgs a) {
 
     int L = seq_len_of(a, b);
     if (L > a.cap) L = a.cap;
+
+    // Fused append: the split that covers the new position (the last split
+    // if it lies beyond them) writes the row into its page before its first
+    // K/V load and waits for the stores to complete, so its own loads of that
+    // row return it -- the reference appends before it attends
+    // (forward_gpu.cu:593-640), and only this workgroup reads that row.
+    // Invalid positions and page ids are dropped as by kvhp_paged_append_kv.
+    if constexpr (PAGED) {
+        if (a.k_new) {
+            const int p = a.new_pos[b];
+            const int writer = p >= 0 ? min(p / a.chunk, a.nsplit - 1) : -1;
+            if (split == writer) {
+                constexpr int LPR0 = D / 8;
+                const int pid = (p >> 4) < a.k.max_pages
+                                    ? a.k.bt[(int64_t)b * a.k.max_pages + (p >> 4)] : -1;
+                if (pid >= 0 && pid < a.k.num_pages && lane < LPR0) {
+                    const int64_t src = ((int64_t)b * a.Hkv + kvh) * D + 8 * lane;
+                    const int64_t dst = kvh * a.k.stride_h +
+                                        ((int64_t)pid * kPage + (p & 15)) * a.k.stride_s + 8 * lane;
+                    store_half8(a.pool_k + dst, load_half8(a.k_new + src));
+                    store_half8(a.pool_v + dst, load_half8(a.v_new + src));
+                }
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+        }
+    }
+
     if (L <= 0) {
         if (split == 0) {
             const half8 z = {};
@@ -705,10 +740,14 @@ int validate_view(const kvhp_kv_view* v, const char* name) {
 }  // namespace
 
 // seq_lens == nullptr: every sequence has length fixed_len (host value).
+// k_new != nullptr: fused paged append (paged views only) -- row b of
+// k_new / v_new [B][Hkv][D] goes to position new_pos[b] before attention.
 int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_view* vv,
                           const int32_t* seq_lens, int fixed_len, void* out, int batch,
                           int hq, int hkv, int d, int max_seq_len, int num_splits,
-                          void* workspace, size_t workspace_bytes, hipStream_t s) {
+                          void* workspace, size_t workspace_bytes, hipStream_t s,
+                          const void* k_new = nullptr, const void* v_new = nullptr,
+                          const int32_t* new_pos = nullptr) {
     if (batch <= 0 || max_seq_len <= 0) return KVHP_OK;
     KVHP_REQUIRE(q && out, KVHP_ERR_INVALID, "decode_attention: null pointer");
     KVHP_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0, KVHP_ERR_INVALID,
@@ -735,6 +774,11 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
     a.Hq = hq;
     a.Hkv = hkv;
     a.scale_log2 = 1.4426950408889634f / std::sqrt(static_cast<float>(d));
+    a.k_new = nullptr;
+    a.v_new = nullptr;
+    a.new_pos = nullptr;
+    a.pool_k = const_cast<f16*>(static_cast<const f16*>(kv->data));
+    a.pool_v = const_cast<f16*>(static_cast<const f16*>(vv->data));
 
     // The fast kernel reads one block table for K and V (one page id per
     // token position, the layout PagedKVCache builds).
@@ -745,6 +789,22 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
     const bool fast = (d == 64 || d == 128) && fast_group(G) && view_fast_ok(*kv) &&
                       view_fast_ok(*vv) && aligned16(q) && aligned16(out) && shared_table &&
                       plan.nsplit <= kMaxSplits;
+    if (k_new) {
+        KVHP_REQUIRE(paged && v_new && new_pos, KVHP_ERR_INVALID,
+                     "append_decode: paged views, k_new, v_new and positions required");
+        if (fast && aligned16(k_new) && aligned16(v_new)) {
+            a.k_new = static_cast<const f16*>(k_new);
+            a.v_new = static_cast<const f16*>(v_new);
+            a.new_pos = new_pos;
+        } else {
+            // outside the fused kernel's shapes: the append, then attention
+            rc = kvhp_paged_append_kv(k_new, v_new, const_cast<void*>(kv->data),
+                                      const_cast<void*>(vv->data), kv->block_table,
+                                      kv->max_pages, new_pos, batch, 1, hkv, d, kv->num_pages,
+                                      s);
+            if (rc) return rc;
+        }
+    }
     if (!fast) {
         // Single pass: every sequence fully, no workspace.
         a.ws_o = nullptr;
@@ -837,6 +897,23 @@ extern "C" int kvhp_decode_attention(const void* q, const kvhp_kv_view* k_view,
     return decode_attention_impl(q, k_view, v_view, seq_lens, 0, out, batch, num_q_heads,
                                  num_kv_heads, head_dim, max_seq_len, num_splits, workspace,
                                  workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvhp_paged_append_decode(const void* q, const void* k_new, const void* v_new,
+                                        const kvhp_kv_view* k_view, const kvhp_kv_view* v_view,
+                                        const int32_t* positions, const int32_t* seq_lens,
+                                        void* out, int batch, int num_q_heads, int num_kv_heads,
+                                        int head_dim, int max_seq_len, int num_splits,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    KVHP_REQUIRE(seq_lens && k_new && v_new && positions && k_view && v_view, KVHP_ERR_INVALID,
+                 "append_decode: null pointer");
+    KVHP_REQUIRE(k_view->block_table && v_view->block_table, KVHP_ERR_INVALID,
+                 "append_decode: paged views required");
+    return decode_attention_impl(q, k_view, v_view, seq_lens, 0, out, batch, num_q_heads,
+                                 num_kv_heads, head_dim, max_seq_len, num_splits, workspace,
+                                 workspace_bytes, static_cast<hipStream_t>(stream), k_new, v_new,
+                                 positions);
 }
 
 extern "C" int kvhp_decode_gqa(const void* q, const void* k_cache, const void* v_cache,

@@ -72,6 +72,9 @@ _SIGNATURES = {
     "kvhp_decode_workspace_init": (_i32, [_vp, _sz, _vp]),
     "kvhp_decode_attention": (_i32, [_vp, ctypes.POINTER(KVView), ctypes.POINTER(KVView), _vp,
                                      _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "kvhp_paged_append_decode": (_i32, [_vp, _vp, _vp, ctypes.POINTER(KVView),
+                                        ctypes.POINTER(KVView), _vp, _vp, _vp, _i32, _i32, _i32,
+                                        _i32, _i32, _i32, _vp, _sz, _vp]),
     "kvhp_decode_gqa": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "kvhp_flash_prefill": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "kvhp_flash_prefill_paged": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp,
@@ -222,6 +225,19 @@ def decode_attention(q, k_view: KVView, v_view: KVView, seq_lens, out, num_q_hea
         _ptr(q), ctypes.byref(k_view), ctypes.byref(v_view), _ptr(seq_lens), _ptr(out),
         seq_lens.shape[0], num_q_heads, num_kv_heads, head_dim, max_seq_len, num_splits,
         _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+def paged_append_decode(q, k_new, v_new, k_view: KVView, v_view: KVView, positions, seq_lens,
+                        out, num_q_heads, num_kv_heads, head_dim, max_seq_len, num_splits=0,
+                        workspace=None, stream=None):
+    """Append row b of k_new / v_new [B][Hkv][D] at positions[b], then decode
+    attention over seq_lens[b] keys (one call; paged views)."""
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(load().kvhp_paged_append_decode(
+        _ptr(q), _ptr(k_new), _ptr(v_new), ctypes.byref(k_view), ctypes.byref(v_view),
+        _ptr(positions), _ptr(seq_lens), _ptr(out), seq_lens.shape[0], num_q_heads,
+        num_kv_heads, head_dim, max_seq_len, num_splits, _ptr(workspace), ws_bytes,
+        _stream(stream)))
 
 
 def decode_gqa(q, k_cache, v_cache, out, total_seq_len, num_q_heads, num_kv_heads, max_seq,

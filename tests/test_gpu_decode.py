@@ -227,3 +227,47 @@ def test_decode_caller_workspace_reuse_and_empty_sequences():
                                       vc.astype(np.float32), np.array(lens, np.int32), hq, hkv, d)
         assert_attn_close(got, ref, f"lens={lens}")
         assert np.all(got[np.array(lens) == 0] == 0)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (32, 4, 64), (12, 4, 96)])
+def test_paged_append_decode_matches_separate_calls(hq, hkv, d):
+    """kvhp_paged_append_decode (one call: the covering split writes the new
+    row into its page and attends it from registers) against
+    kvhp_paged_append_kv followed by kvhp_decode_attention, bit for bit on
+    both the pools and the outputs.  Ragged batch: an empty sequence, rows
+    on page boundaries, a new position past the attended length (written,
+    not attended), and a new position on an unallocated page (dropped).
+    D=96 runs the fallback (append kernel, then the generic decode)."""
+    import torch
+    rng = np.random.default_rng(500 + d)
+    lens = np.array([1000, 0, 1, 15, 16, 300, 2047], np.int32)   # cached tokens
+    b = lens.size
+    bt, P = make_block_tables(rng, lens + 8)
+    pos = lens.copy()
+    seq = lens + 1
+    pos[5] = lens[5] + 4          # written, beyond the attended keys
+    seq[5] = lens[5]
+    bt[3, pos[3] // 16] = -1      # no page for this row: the write is dropped
+    pool_k = to_gpu_f16(oracle.normal_f16(rng, (hkv, P, 16, d)))
+    pool_v = to_gpu_f16(oracle.normal_f16(rng, (hkv, P, 16, d)))
+    k_new = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, d)))
+    v_new = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, d)))
+    q = to_gpu_f16(oracle.normal_f16(rng, (b, hq, d)))
+    bt_t, pos_t, seq_t = to_gpu(bt), to_gpu(pos), to_gpu(seq)
+    cap = int(seq.max())
+    note(f"append_decode Hq={hq} Hkv={hkv} D={d} lens={lens.tolist()}")
+
+    pk1, pv1 = pool_k.clone(), pool_v.clone()
+    out1 = torch.full((b, hq, d), float("nan"), dtype=torch.float16, device="cuda")
+    kvhp.paged_append_kv(k_new.view(b, 1, hkv, d), v_new.view(b, 1, hkv, d), pk1, pv1, bt_t, pos_t,
+                         b, 1, hkv, d)
+    kvhp.decode_attention(q, kvhp.paged_view(pk1, bt_t), kvhp.paged_view(pv1, bt_t), seq_t, out1,
+                          hq, hkv, d, cap)
+    pk2, pv2 = pool_k.clone(), pool_v.clone()
+    out2 = torch.full((b, hq, d), float("nan"), dtype=torch.float16, device="cuda")
+    kvhp.paged_append_decode(q, k_new, v_new, kvhp.paged_view(pk2, bt_t),
+                             kvhp.paged_view(pv2, bt_t), pos_t, seq_t, out2, hq, hkv, d, cap)
+    sync()
+    assert torch.equal(pk1, pk2) and torch.equal(pv1, pv2), "pools differ"
+    assert torch.equal(out1, out2), "outputs differ"
+    assert not torch.equal(pk2, pool_k), "nothing was appended"
