@@ -130,6 +130,20 @@ inline void paged_append_kv(const half* src_k, const half* src_v, half* pool_k, 
                                     num_pages, stream));
 }
 
+// The serving step's append + decode in one call (kvhp_paged_append_decode):
+// row b of k_new / v_new [B][Hkv][D] goes to position positions[b] through
+// the views' block table, then decode attention over seq_lens[b] keys.
+inline void paged_append_decode(const half* q, const half* k_new, const half* v_new,
+                                const KVView& k_view, const KVView& v_view,
+                                const int32_t* positions, const int32_t* seq_lens, half* out,
+                                int batch_size, int num_q_heads, int num_kv_heads, int head_dim,
+                                int max_seq_len, Stream stream = nullptr) {
+    KVHP_CHECK(kvhp_paged_append_decode(q, k_new, v_new, k_view.c_view(), v_view.c_view(),
+                                        positions, seq_lens, out, batch_size, num_q_heads,
+                                        num_kv_heads, head_dim, max_seq_len, 0, nullptr, 0,
+                                        stream));
+}
+
 // Paged gather into contiguous out [B][Hkv][max_len][D] (zeros past
 // seq_lens[b]).
 inline void paged_gather_kv(const half* pool_k, const half* pool_v, const int32_t* block_tables,

@@ -273,6 +273,16 @@ public:
                               num_q_heads, num_kv_heads_, head_dim_, max_seq_len, nullptr, stream);
     }
 
+    // One decode token per slot: append k_new / v_new [batch][Hkv][D] at each
+    // slot's write position, then attend q over each slot's seq_len keys,
+    // in one call (append and decode of the same step, fused).
+    void append_decode(int layer, const half* k_new, const half* v_new, const half* q, half* out,
+                       int batch, int num_q_heads, int max_seq_len, Stream stream = nullptr) {
+        hip::paged_append_decode(q, k_new, v_new, k_view(layer), v_view(layer),
+                                 write_positions(), seq_lens(), out, batch, num_q_heads,
+                                 num_kv_heads_, head_dim_, max_seq_len, stream);
+    }
+
     int num_layers() const { return num_layers_; }
     int num_kv_heads() const { return num_kv_heads_; }
     int head_dim() const { return head_dim_; }

@@ -415,8 +415,12 @@ void case_paged_serving_steps() {
             DeviceBuffer<half> out(q.size());
             int max_len = 0;
             for (int s = 0; s < B; ++s) max_len = std::max(max_len, cache.seq_len(s));
-            cache.append(0, dk.data(), dv.data(), B, 1);
-            cache.decode(0, dq.data(), out.data(), B, hq, max_len);
+            if (st % 2 == 0) {  // separate calls, then the fused step, alternately
+                cache.append(0, dk.data(), dv.data(), B, 1);
+                cache.decode(0, dq.data(), out.data(), B, hq, max_len);
+            } else {
+                cache.append_decode(0, dk.data(), dv.data(), dq.data(), out.data(), B, hq, max_len);
+            }
             HIP_CHECK(hipDeviceSynchronize());
             // oracle over the contiguous history [B][hkv][max_len][d]
             std::vector<float> kc((size_t)B * hkv * max_len * d, 0.f), vc(kc.size(), 0.f);
