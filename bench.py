@@ -14,16 +14,17 @@ value = algorithmic bytes of the step (decode: K+V of every cached token once,
 q read, out write, block-table and length reads; append: new K/V read + write)
 divided by the measured step time.  roofline = that call (split kernel +
 merge kernel), timed with HIP events on its stream inside the timed region.
-cpu_baseline = the
-oracle's restatement of the reference CPU attention arithmetic
-(oracle/kvhp_oracle.c) on the same inputs, on the host cores.
+cpu_baseline = the oracle's restatement of the reference CPU attention
+arithmetic (oracle/kvhp_oracle.c) on the same inputs, on the host cores.
 
 Also reported under "extra" (each measured with L2+MALL flushed by a 1 GiB
 read before every rep unless labelled warm): config 1 (decode at ctx 512),
 config 2 (ctx 4K/16K/64K x splits 1/4/16/64), config 4 (causal prefill
 S=512/2048/8192, TFLOP/s vs fp16 MFMA peak), config 5 (Llama-style 1.1B:
 2048-id prefill, then 128 greedy decode steps, tok/s and the HBM bytes of a
-step against 8 TB/s; also top-level as config5_decode_tok_s).
+step against 8 TB/s; also top-level as config5_decode_tok_s), and the KV
+movement kernels alone (paged gather of the config-3 pool, 2048-token
+appends).
 """
 import argparse
 import json
@@ -53,7 +54,7 @@ def parse():
     ap.add_argument("--splits", type=int, default=0, help="decode split count (0 = auto)")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 2 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5")
+    ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5,kv")
     ap.add_argument("--profile", nargs="?", const="decode", default=None,
                     choices=("decode", "prefill", "c5"),
                     help="short run for rocprofv3: a 256 MiB device copy (counter "
@@ -237,6 +238,49 @@ def run_config3(torch, kvhp, args):
 
 
 # ---------------------------------------------------------------- extras ----
+def run_kv_movement(torch, kvhp):
+    """KV movement kernels on their own (flushed): paged gather of the config-3
+    pool into contiguous [B][Hkv][cap][D] K and V (bit-exact copy, zeros past
+    each length), and a 2048-token prompt's K/V appended into 16-token pages
+    (paged) or a head-major cache (contiguous)."""
+    c = build_config3(torch, kvhp)
+    b, hkv, d = c["b"], c["hkv"], c["d"]
+    L1 = c["lens"] + 1
+    cap = int(L1.max())
+    ok = torch.empty((b, hkv, cap, d), dtype=torch.float16, device="cuda")
+    ov = torch.empty_like(ok)
+    fl = Flusher(torch)
+    g = time_op(torch, lambda: kvhp.paged_gather_kv(c["pool_k"], c["pool_v"], c["bt"], c["lens1"],
+                                                    cap, ok, ov), 10, fl)[0]
+    g_read = int(L1.sum()) * hkv * d * 2 * 2
+    g_write = b * hkv * cap * d * 2 * 2
+    del ok, ov, c
+    torch.cuda.empty_cache()
+    S, hkv2, d2 = 2048, 8, 128
+    src_k = torch.randn((1, S, hkv2, d2), device="cuda").half()
+    src_v = torch.randn_like(src_k)
+    P = S // 16 + 4
+    pk = torch.zeros((hkv2, P, 16, d2), dtype=torch.float16, device="cuda")
+    pv = torch.zeros_like(pk)
+    bt = torch.arange(P, dtype=torch.int32, device="cuda").view(1, P)
+    zero = torch.zeros(1, dtype=torch.int32, device="cuda")
+    a_p = time_op(torch, lambda: kvhp.paged_append_kv(src_k, src_v, pk, pv, bt, zero, 1, S, hkv2,
+                                                      d2), 20, fl)[0]
+    ck = torch.zeros((hkv2, S, d2), dtype=torch.float16, device="cuda")
+    cv = torch.zeros_like(ck)
+    a_c = time_op(torch, lambda: kvhp.append_kv(src_k, src_v, ck, cv, S, 0, hkv2, S, d2), 20, fl)[0]
+    a_bytes = 2 * S * hkv2 * d2 * 2 * 2
+    return {"workload": "paged gather of the config-3 pool (32 seqs, sum L=%d) into contiguous "
+                        "K/V [32][8][%d][128]; append of 2048 tokens x 8 heads x D=128" % (
+                            int(L1.sum()), cap),
+            "gather_us": round(g, 2), "gather_bytes": g_read + g_write,
+            "gather_GBps": round((g_read + g_write) / g / 1e3, 1),
+            "paged_append_2048_us": round(a_p, 2),
+            "contig_append_2048_us": round(a_c, 2), "append_bytes": a_bytes,
+            "paged_append_GBps": round(a_bytes / a_p / 1e3, 1),
+            "contig_append_GBps": round(a_bytes / a_c / 1e3, 1)}
+
+
 def run_config1(torch, kvhp):
     hq, hkv, d, max_seq = 32, 8, 64, 512
     g = torch.Generator(device="cuda").manual_seed(1)
@@ -472,8 +516,11 @@ def main():
     del c
     torch.cuda.empty_cache()
     extra = {}
-    parts = set(args.only.split(",")) if args.only else {"c1", "c2", "c4", "c5"}
+    parts = set(args.only.split(",")) if args.only else {"c1", "c2", "c4", "c5", "kv"}
     if not args.no_extra:
+        if "kv" in parts:
+            log("kv movement ...")
+            extra["kv_movement"] = run_kv_movement(torch, kvhp)
         if "c1" in parts:
             log("config1 ...")
             extra["config1"] = run_config1(torch, kvhp)

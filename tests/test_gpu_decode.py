@@ -112,9 +112,11 @@ def test_config2_64k_split_sweep_and_invariance():
         assert np.max(np.abs(o - outs[0])) <= 2e-3
 
 
-def _paged_case(rng, b, lens, hq, hkv, d, with_append):
+def _paged_case(rng, b, lens, hq, hkv, d, with_append, fused=False):
     """Builds a paged pool from token-major K/V through the oracle's paged
-    append (host), returns GPU output and oracle reference."""
+    append (host), returns GPU output and oracle reference.  with_append: the
+    step's new token goes in on the GPU, by the append kernel or (fused) by
+    kvhp_paged_append_decode itself."""
     import torch
     lens = np.asarray(lens, np.int32)
     bt, P = make_block_tables(rng, lens + 1)
@@ -131,15 +133,20 @@ def _paged_case(rng, b, lens, hq, hkv, d, with_append):
     pk_t = to_gpu(pk.view(np.float16))
     pv_t = to_gpu(pv.view(np.float16))
     bt_t = to_gpu(bt)
-    if with_append:   # the step's new token goes in with the GPU append kernel
-        newk = np.ascontiguousarray(tk[np.arange(b), lens])[:, None]
-        newv = np.ascontiguousarray(tv[np.arange(b), lens])[:, None]
-        kvhp.paged_append_kv(to_gpu_f16(newk), to_gpu_f16(newv), pk_t, pv_t, bt_t,
-                             to_gpu(lens), b, 1, hkv, d)
     L1 = lens + 1
     out = torch.empty((b, hq, d), dtype=torch.float16, device="cuda")
-    kvhp.decode_attention(to_gpu_f16(q), kvhp.paged_view(pk_t, bt_t), kvhp.paged_view(pv_t, bt_t),
-                          to_gpu(L1), out, hq, hkv, d, int(L1.max()))
+    kview, vview = kvhp.paged_view(pk_t, bt_t), kvhp.paged_view(pv_t, bt_t)
+    newk = np.ascontiguousarray(tk[np.arange(b), lens])
+    newv = np.ascontiguousarray(tv[np.arange(b), lens])
+    if with_append and fused:
+        kvhp.paged_append_decode(to_gpu_f16(q), to_gpu_f16(newk), to_gpu_f16(newv), kview, vview,
+                                 to_gpu(lens), to_gpu(L1), out, hq, hkv, d, int(L1.max()))
+    else:
+        if with_append:   # the step's new token goes in with the GPU append kernel
+            kvhp.paged_append_kv(to_gpu_f16(newk[:, None]), to_gpu_f16(newv[:, None]), pk_t, pv_t,
+                                 bt_t, to_gpu(lens), b, 1, hkv, d)
+        kvhp.decode_attention(to_gpu_f16(q), kview, vview, to_gpu(L1), out, hq, hkv, d,
+                              int(L1.max()))
     sync()
     kc = contiguous_from_tokens(tk.astype(np.float32), L1, int(L1.max()))
     vc = contiguous_from_tokens(tv.astype(np.float32), L1, int(L1.max()))
@@ -157,14 +164,16 @@ def test_paged_decode_with_append(b, maxlen, hq, hkv, d):
     assert_attn_close(got, ref, "paged")
 
 
-def test_config3_paged_decode_full_size():
+@pytest.mark.parametrize("fused", [False, True])
+def test_config3_paged_decode_full_size(fused):
     """BASELINE config 3 at full size: 32 sequences with seeded lengths in
     [128, 8192], 32/8 heads, D=128, 16-token pages on a seeded random
-    permutation; one appended token per sequence, then decode."""
+    permutation; one appended token per sequence, then decode -- as two
+    calls, or as the one kvhp_paged_append_decode call the bench times."""
     rng = np.random.default_rng(3)
     lens = rng.integers(128, 8193, size=32) - 1   # + the appended token
-    note(f"config3 full: sum L={int(lens.sum()) + 32}")
-    got, ref = _paged_case(rng, 32, lens, 32, 8, 128, with_append=True)
+    note(f"config3 full (fused={fused}): sum L={int(lens.sum()) + 32}")
+    got, ref = _paged_case(rng, 32, lens, 32, 8, 128, with_append=True, fused=fused)
     assert_attn_close(got, ref, "config3")
 
 
