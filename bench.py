@@ -17,8 +17,9 @@ merge kernel), timed with HIP events on its stream inside the timed region.
 cpu_baseline = the oracle's restatement of the reference CPU attention
 arithmetic (oracle/kvhp_oracle.c) on the same inputs, on the host cores.
 
-Also reported under "extra" (each measured with L2+MALL flushed by a 1 GiB
-read before every rep unless labelled warm): config 1 (decode at ctx 512),
+Also reported under "extra" (each measured with L2+MALL flushed by a 512 MB
+write and a 1 GiB read before every rep unless labelled warm): config 1
+(decode at ctx 512),
 config 2 (ctx 4K/16K/64K x splits 1/4/16/64), config 4 (causal prefill
 S=512/2048/8192, TFLOP/s vs fp16 MFMA peak), config 5 (Llama-style 1.1B:
 2048-id prefill, then 128 greedy decode steps, tok/s and the HBM bytes of a
@@ -65,14 +66,16 @@ def parse():
 
 
 class Flusher:
-    """Reads 1 GiB (4x the 256 MB MALL) to evict L2 and MALL between reps.
-    A read leaves clean lines behind, so the timed kernel does not pay for
-    writing back the flush's own data."""
+    """Evicts L2 and MALL (256 MB) between reps: writes 512 MB, then reads
+    1 GiB, so the written lines are written back before the timed region
+    and the timed kernel does not pay for the flush's own dirty data."""
 
     def __init__(self, torch):
+        self.wbuf = torch.empty(1 << 27, dtype=torch.float32, device="cuda")
         self.buf = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
 
     def __call__(self):
+        self.wbuf.fill_(1.0)
         self.buf.sum()
 
 
@@ -134,9 +137,35 @@ def build_config3(torch, kvhp, seed=3):
                 out=torch.empty((b, hq, d), dtype=torch.float16, device=dev))
 
 
+def host_cpu_info():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
+
+
+def time_cpu(fn, min_reps, min_seconds):
+    """Median seconds of fn over at least min_reps runs (and min_seconds),
+    after one warm-up run."""
+    fn()
+    ts, t_all = [], time.perf_counter()
+    while len(ts) < min_reps or time.perf_counter() - t_all < min_seconds:
+        t0 = time.perf_counter()
+        out = fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), len(ts), out
+
+
 def cpu_baseline_config3(c, torch):
     """Oracle decode (reference attention arithmetic restated in C) on the
-    same step's inputs, all host threads; sample = the full 32-sequence step."""
+    same step's inputs: the full 32-sequence step, median of >= 5 runs after
+    a warm-up, on all host threads (up to 16, the box's share) and on one."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     b, hq, hkv, d = c["b"], c["hq"], c["hkv"], c["d"]
@@ -152,23 +181,65 @@ def cpu_baseline_config3(c, torch):
     del kv_k, kv_v
     qf = c["q"].float().cpu().numpy()
     threads = min(16, os.cpu_count() or 1)
-    oracle.decode_attention(qf, kf[:1, :, :64], vf[:1, :, :64], np.array([64], np.int32), hq,
-                            hkv, d, threads)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:   # whole steps until at least 2 s of CPU work
-        ref = oracle.decode_attention(qf, kf, vf, L1, hq, hkv, d, threads)
-        reps += 1
-        dt = time.perf_counter() - t0
-        if dt >= 2.0:
-            break
-    nbytes = decode_bytes(L1, hq, hkv, d) * reps
+    nbytes = decode_bytes(L1, hq, hkv, d)
+    med, reps, ref = time_cpu(lambda: oracle.decode_attention(qf, kf, vf, L1, hq, hkv, d, threads),
+                              5, 2.0)
+    med1, reps1, _ = time_cpu(lambda: oracle.decode_attention(qf, kf, vf, L1, hq, hkv, d, 1), 5, 0.0)
     gpu_out = c["out"].float().cpu().numpy()
     err = float(np.abs(gpu_out - ref).max())
-    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": f"full config-3 decode (32 seqs, sum L={int(L1.sum())}), {reps} reps in "
-                      f"{dt:.2f} s; oracle max-abs diff vs GPU output {err:.2e}",
-            "seconds": round(dt, 3)}
+            "sample": f"full config-3 decode step (32 seqs, sum L={int(L1.sum())}), median of "
+                      f"{reps} runs {med * 1e3:.1f} ms; oracle max-abs diff vs GPU output "
+                      f"{err:.2e}",
+            "us_per_step": round(med * 1e6, 1),
+            "one_thread": {"value": round(nbytes / med1 / 1e9, 3), "unit": "GB/s",
+                           "us_per_step": round(med1 * 1e6, 1), "runs": reps1},
+            **host_cpu_info()}
+
+
+def cpu_baseline_config5(torch, kvhp, prompt_len=16, steps=2):
+    """The decoder oracle (reference CPU forward restated, with a K/V cache)
+    on the config-5 model's weights read back from the GPU: a seeded
+    prompt_len-id prefill, then `steps` greedy decode steps, all host threads
+    (up to 16).  Bounded sample: the decode step's cost is dominated by the
+    2.07 GB of weights, not by the short context."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from llama_oracle import LlamaOracle
+    cfg = kvhp.llama_1b_config()
+    model = kvhp.LlamaModel(cfg, seed=5, max_ctx=prompt_len + steps + 1)
+    f32 = lambda t: t.astype(np.float32)
+    v, hdim, f = cfg.vocab_size, cfg.hidden_size, cfg.ffn_size
+    nqkv = (cfg.num_q_heads + 2 * cfg.num_kv_heads) * cfg.head_dim
+    w = {"embed": f32(model.tensor(-1, kvhp.LLAMA_EMBED)).reshape(v, hdim),
+         "lm_head": f32(model.tensor(-1, kvhp.LLAMA_LM_HEAD)).reshape(v, hdim),
+         "final_norm": f32(model.tensor(-1, kvhp.LLAMA_FINAL_NORM)), "layers": []}
+    for li in range(cfg.num_layers):
+        w["layers"].append({
+            "attn_norm": f32(model.tensor(li, kvhp.LLAMA_ATTN_NORM)),
+            "ffn_norm": f32(model.tensor(li, kvhp.LLAMA_FFN_NORM)),
+            "w_qkv": f32(model.tensor(li, kvhp.LLAMA_W_QKV)).reshape(nqkv, hdim),
+            "w_o": f32(model.tensor(li, kvhp.LLAMA_W_O)).reshape(hdim, hdim),
+            "w_gate_up": f32(model.tensor(li, kvhp.LLAMA_W_GATE_UP)).reshape(2 * f, hdim),
+            "w_down": f32(model.tensor(li, kvhp.LLAMA_W_DOWN)).reshape(hdim, f)})
+    model.close()
+    threads = min(16, os.cpu_count() or 1)
+    ref = LlamaOracle(cfg, w, nthreads=threads)
+    prompt = np.random.default_rng(5).integers(0, v, prompt_len).astype(np.int32)
+    t0 = time.perf_counter()
+    logits = ref.forward(prompt)
+    t_prefill = time.perf_counter() - t0
+    per_tok = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        logits = ref.forward([int(np.argmax(logits))])
+        per_tok.append(time.perf_counter() - t0)
+    s_tok = float(np.median(per_tok))
+    return {"value": round(1.0 / s_tok, 3), "unit": "tok/s", "s_per_token": round(s_tok, 3),
+            "cores": threads, "kind": "port",
+            "sample": f"{prompt_len}-id prefill ({t_prefill:.2f} s, reported separately) then "
+                      f"{steps} greedy decode steps, median",
+            "prefill_s": round(t_prefill, 3)}
 
 
 def run_config3(torch, kvhp, args):
@@ -507,7 +578,7 @@ def main():
                          dbytes / r["decode_only_us_flushed_median"] / 1e3, 1),
                      "note": "achieved = algorithmic bytes of the step / mean HIP-event time of "
                              "the one call in the timed loop (working set 504 MB vs 256 MB "
-                             "MALL); flushed = after a 1 GiB read; separate = the same step as "
+                             "MALL); flushed = after a 512 MB write + 1 GiB read; separate = the same step as "
                              "kvhp_paged_append_kv + kvhp_decode_attention"},
     }
     if not args.no_cpu:
@@ -534,6 +605,9 @@ def main():
             log("config5 ...")
             extra["config5"] = run_config5(torch, kvhp)
             line["config5_decode_tok_s"] = extra["config5"]["decode_tok_s"]
+            if not args.no_cpu:
+                log("config5 cpu baseline ...")
+                extra["config5"]["cpu_baseline"] = cpu_baseline_config5(torch, kvhp)
     line["extra"] = extra
     print(json.dumps(line))
 
