@@ -1,11 +1,13 @@
 // prefill.hip -- causal flash attention for prefill on CDNA4 fp16 MFMA (gfx950).
 //
 // Work decomposition: a 512-thread workgroup (8 waves) owns one KV head and
-// a query block of 16*RB rows for all G query heads of that KV head -- G*RB
-// = 8 units of (head, 16 rows), one unit per wave (RB = 8/G).  Each 64-key
-// K/V tile is read from HBM once per workgroup and consumed by all 8 waves,
-// so GQA heads share their K/V traffic.  Query blocks i and N-1-i are
-// processed by the same workgroup, giving every workgroup the same causal
+// a query block of 32*RB rows for all G query heads of that KV head: G*RB
+// units of (head, 32 rows).  With KG = 1 each wave owns one unit (RB = 8/G);
+// for short prompts (KG = 2, G <= 4) two wave groups share the units and
+// split every tile's keys, doubling the workgroup count.  Each 64-key K/V
+// tile is read from HBM once per workgroup and consumed by all 8 waves, so
+// GQA heads share their K/V traffic.  Query blocks i and N-1-i are processed
+// by the same workgroup (two passes), giving every workgroup the same causal
 // work; grid x enumerates (pair, kv_head) with the kv head fastest.
 //
 // K/V staging: a 4-stage LDS ring (4 x 32 KB for D=128), filled by
@@ -16,19 +18,18 @@
 // swizzle of their 16-byte chunks so that both the K reads (ds_read_b128)
 // and the transposing V reads (ds_read_b64_tr_b16) are bank-conflict free.
 //
-// Per tile and unit, the contraction runs transposed so that one lane owns one
-// query row for the whole online softmax:
-//   S^T = K Q^T     v_mfma_f32_16x16x32_f16, A = K rows from LDS, B = Q^T
-//                   held in registers.  Lane l gets keys 4(l/16)+e of each
-//                   16-key block for query row l%16.
+// Per tile and unit, on v_mfma_f32_32x32x16_f16, transposed so that one lane
+// owns one query row for the whole online softmax:
+//   S^T = K Q^T     A = K rows from LDS, B = Q^T held in registers; the S^T of
+//                   tile t+1 is computed before the softmax of tile t.
 //   softmax         fp32 in the log2 domain; the causal mask is applied only on
-//                   tiles that cross the diagonal; the running max is taken on
-//                   raw scores and the rescale of O is skipped when no row's
-//                   max moved.
+//                   tiles that cross the diagonal; the running max moves (and
+//                   O is rescaled) only when a row's max passes it by 8 in
+//                   log2 units, so P <= 256 stays exact in fp16; row sums by
+//                   v_dot2_f32_f16 over the fp16 P.
 //   O^T += V^T P^T  A = V^T read with ds_read_b64_tr_b16 (transposing 8-byte
-//                   LDS reads), B = P^T converted to fp16 straight from the S^T
-//                   accumulators: k-slot (g,e') of a 32-key step is key
-//                   4g+e' (e'<4) or 16+4g+e'-4 in both operands.
+//                   LDS reads), B = P^T converted to fp16 straight from the
+//                   S^T accumulators.
 //
 // With a page pool, each workgroup also writes the K/V rows of its own query
 // block into the pages after its outputs (every key row is written exactly
