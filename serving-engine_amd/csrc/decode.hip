@@ -428,7 +428,7 @@ decode_merge_kernel(const DecodeArgs a) {
     constexpr int LPR = D / 8;          // lanes per head row (8 dims each)
     constexpr int HPP = kWave / LPR;    // heads per pass of one wave
     constexpr int NP = (G + HPP - 1) / HPP;
-    constexpr int U = 4;                // splits in flight per lane
+    constexpr int U = 8;                // splits in flight per lane (32 per round)
     __shared__ __attribute__((aligned(16))) float red_o[kMergeWaves - 1][NP][kWave][8];
     __shared__ float red_ms[kMergeWaves - 1][NP][kWave][2];
 
