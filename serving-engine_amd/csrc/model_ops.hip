@@ -88,12 +88,13 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
     bool ok[RW];
     const int wv = blockIdx.x;
     if constexpr (EPI == kEpiQKV) {
-        // head hh, pair block pb: rows hh*D + 4pb + i and hh*D + D/2 + 4pb + i
-        const int wph = a.D / 8;
+        // head hh, pair block pb: rows hh*D + (RW/2)pb + i and
+        // hh*D + D/2 + (RW/2)pb + i, i < RW/2
+        const int wph = a.D / RW;
         const int hh = wv / wph, pb = wv % wph;
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
-            row[i] = hh * a.D + (i < RW / 2 ? 0 : a.D / 2) + 4 * pb + (i % (RW / 2));
+            row[i] = hh * a.D + (i < RW / 2 ? 0 : a.D / 2) + (RW / 2) * pb + (i % (RW / 2));
             ok[i] = true;
         }
     } else if constexpr (EPI == kEpiSwiglu) {
@@ -148,9 +149,9 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
     if constexpr (EPI == kEpiQKV) {
         // The angle depends only on the position and the pair: computed here,
         // under the weight loads, instead of after the products.
-        const int hh = wv / (a.D / 8);
+        const int hh = wv / (a.D / RW);
         if (hh < a.Hq + a.Hkv) {
-            rope_cs(pos < 0 ? 0 : pos, 4 * (wv % (a.D / 8)) + lane, a.D, a.theta, rc, rs);
+            rope_cs(pos < 0 ? 0 : pos, (RW / 2) * (wv % (a.D / RW)) + lane, a.D, a.theta, rc, rs);
             asm volatile("" ::"v"(rc), "v"(rs));
         }
     }
@@ -191,9 +192,9 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
                 x1 = round16(acc[i]);
                 x2 = round16(acc[RW / 2 + i]);
             }
-        const int wph = a.D / 8;
+        const int wph = a.D / RW;
         const int hh = wv / wph, pb = wv % wph;
-        const int d = 4 * pb + lane;          // pair (d, d + D/2)
+        const int d = (RW / 2) * pb + lane;   // pair (d, d + D/2)
         const int half = a.D / 2;
         if (hh >= a.Hq + a.Hkv) {             // v: no rotation
             const int kvh = hh - a.Hq - a.Hkv;
@@ -334,18 +335,21 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
     else
         units = a.N;
     const bool xa = aligned16(a.x) && aligned16(a.W) && (!RMS || aligned16(a.norm_w));
+    // Two rows per wave: the decode GEMVs are latency-bound, and more, smaller
+    // waves in flight beat fewer that each stream more rows (measured on the
+    // config-5 step: 1448 tok/s at 2 rows, 1430 at 4, 1376 at 8).
     if (xa && a.K == 2048) {
-        constexpr int RW = 8;
+        constexpr int RW = 2;
         int grid;
         if constexpr (EPI == kEpiQKV)
-            grid = (a.Hq + 2 * a.Hkv) * (a.D / 8);
+            grid = (a.Hq + 2 * a.Hkv) * (a.D / RW);
         else if constexpr (EPI == kEpiSwiglu)
             grid = (a.N + RW / 2 - 1) / (RW / 2);
         else
             grid = (a.N + RW - 1) / RW;
         hipLaunchKernelGGL((gemv_kernel<4, RW, EPI, RMS>), dim3(grid), dim3(kWave), 0, s, a);
     } else if (xa && a.K == 5632 && EPI != kEpiQKV && EPI != kEpiSwiglu) {
-        constexpr int RW = 4;
+        constexpr int RW = 2;
         hipLaunchKernelGGL((gemv_kernel<11, RW, EPI, RMS>), dim3((a.N + RW - 1) / RW),
                            dim3(kWave), 0, s, a);
     } else {
