@@ -201,6 +201,57 @@ def test_decode_gqa_legacy_api(d):
         assert_attn_close(from_gpu(out)[None].astype(np.float32), ref, f"D={d} case {i}")
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (32, 4, 64), (8, 8, 96)])
+def test_decode_known_answers(hq, hkv, d):
+    """Answers fixed by the mathematics, not by the oracle:
+    * L = 1: softmax over one key is 1, so every query head returns V[0] of
+      its KV head bit for bit;
+    * all keys equal: uniform weights, the mean of the V rows;
+    * one key = 12 x the shared query direction: its score leads by ~12 sqrt(D)
+      (every other weight underflows to 0 in fp32), so the output is that
+      key's V row bit for bit, whichever split holds it;
+    * V constant per KV head: head h returns the constant of KV head h // G
+      (the GQA map of decode_attention_split.cu:48-49)."""
+    g = hq // hkv
+    rng = np.random.default_rng(77 + d)
+    note(f"decode KATs Hq={hq} Hkv={hkv} D={d}")
+    # L = 1
+    cap = 64
+    q = oracle.normal_f16(rng, (1, hq, d))
+    kc, vc = oracle.normal_f16(rng, (1, hkv, cap, d)), oracle.normal_f16(rng, (1, hkv, cap, d))
+    got = _run_contig(q, kc, vc, [1], hq, hkv, d, cap)
+    want = np.stack([vc[0, h // g, 0] for h in range(hq)]).astype(np.float32)
+    np.testing.assert_array_equal(got[0], want, err_msg="L=1 must return V[0]")
+    # all keys equal
+    L = 1000
+    kc = np.repeat(oracle.normal_f16(rng, (1, hkv, 1, d)), L, axis=2)
+    vc = oracle.normal_f16(rng, (1, hkv, L, d))
+    got = _run_contig(q, kc, vc, [L], hq, hkv, d, L, splits=4)
+    want = np.stack([vc[0, h // g].astype(np.float64).mean(axis=0) for h in range(hq)])
+    assert_attn_close(got[0], want, "equal keys -> mean of V")
+    # one dominant key, in the middle of a split
+    L, j = 777, 333
+    u = oracle.normal_f16(rng, (d,))
+    q = np.broadcast_to(u, (1, hq, d)).astype(np.float16)
+    kc = (0.1 * oracle.normal_f16(rng, (1, hkv, L, d)).astype(np.float32)).astype(np.float16)
+    kc[0, :, j] = (12.0 * u.astype(np.float32)).astype(np.float16)
+    vc = oracle.normal_f16(rng, (1, hkv, L, d))
+    for splits in (1, 4, 16):
+        got = _run_contig(q, kc, vc, [L], hq, hkv, d, L, splits=splits)
+        want = np.stack([vc[0, h // g, j] for h in range(hq)]).astype(np.float32)
+        np.testing.assert_array_equal(got[0], want, err_msg=f"dominant key, splits={splits}")
+    # GQA map
+    L = 500
+    q = oracle.normal_f16(rng, (1, hq, d))
+    kc = oracle.normal_f16(rng, (1, hkv, L, d))
+    vc = np.empty((1, hkv, L, d), np.float16)
+    for kh in range(hkv):
+        vc[0, kh] = (kh + 1) / 8.0
+    got = _run_contig(q, kc, vc, [L], hq, hkv, d, L)
+    want = np.stack([np.full(d, (h // g + 1) / 8.0) for h in range(hq)])
+    assert_attn_close(got[0], want, "GQA head map")
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(24, 2, 128), (8, 8, 96), (12, 4, 256)])
 def test_decode_generic_shapes(hq, hkv, d):
     """Shapes outside the MFMA kernel's template set (G=12, D=96, D=256) run

@@ -123,6 +123,30 @@ def test_prefill_paged_writes_pages_bit_exact(s, hq, hkv, d):
         assert_attn_close(got[r], ref[r], f"row {r}")
 
 
+@pytest.mark.parametrize("s", [1, 300, 2048])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (32, 4, 64)])
+def test_prefill_known_answers(s, hq, hkv, d):
+    """Answers fixed by the mathematics, not by the oracle: row 0 attends to
+    key 0 alone, so it returns v[0] of its KV head bit for bit (the reference
+    KAT, tests/test_cpu_ops.cpp:112-136); with V constant per KV head every
+    row of head h returns the constant of KV head h // G (the GQA map)."""
+    g = hq // hkv
+    rng = np.random.default_rng(s + d)
+    note(f"prefill KATs S={s} Hq={hq} Hkv={hkv} D={d}")
+    q = oracle.normal_f16(rng, (s, hq, d))
+    k, v = oracle.normal_f16(rng, (s, hkv, d)), oracle.normal_f16(rng, (s, hkv, d))
+    got = _prefill(q, k, v, hq, hkv, d)
+    want = np.stack([v[0, h // g] for h in range(hq)]).astype(np.float32)
+    np.testing.assert_array_equal(got[0], want, err_msg="row 0 must return v[0]")
+    vc = np.empty((s, hkv, d), np.float16)
+    for kh in range(hkv):
+        vc[:, kh] = (kh + 1) / 8.0
+    got = _prefill(q, k, vc, hq, hkv, d)
+    want = np.broadcast_to(np.stack([np.full(d, (h // g + 1) / 8.0) for h in range(hq)]),
+                           (s, hq, d))
+    assert_attn_close(got, want, "GQA head map")
+
+
 def test_causal_gqa_api_routes_to_prefill():
     import torch
     rng = np.random.default_rng(45)
