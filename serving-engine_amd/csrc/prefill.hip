@@ -165,7 +165,10 @@ prefill_mfma_kernel(const PrefillArgs a) {
     constexpr int LPT = 2 * IPW;        // DMA loads per wave per tile (K + V)
     constexpr int TB = kBN * D;         // halfs per tile matrix
     constexpr int KSW = CPR - 1;        // K swizzle: c ^ (r & KSW)
-    constexpr int VSW = CPR / 2 - 1;    // V swizzle: c ^ ((r & VSW) << 1)
+    // V swizzle: the transposing reads of one half-wave touch 4 consecutive
+    // rows x 4 chunks; these land on distinct 16-byte bank groups of the
+    // 256-byte bank line.
+    auto vswz = [](int r) { return CPR == 16 ? 4 * (r & 3) : (r & 3) << 1; };
 
     constexpr int NSTAGE = 4;
     __shared__ __attribute__((aligned(16))) f16 ring[NSTAGE * 2 * TB];
@@ -200,7 +203,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
     for (int p = 0; p < IPW; ++p) {
         const int row = (wave * IPW + p) * RPI + lane / CPR;
         const int ck = (lane % CPR) ^ (row & KSW);
-        const int cv = (lane % CPR) ^ ((row & VSW) << 1);
+        const int cv = (lane % CPR) ^ vswz(row);
         dko[p] = static_cast<uint32_t>((row * kvrs + 8 * ck) * 2);
         dvo[p] = static_cast<uint32_t>((row * kvrs + 8 * cv) * 2);
     }
@@ -225,7 +228,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
                 const int row = blk * RPI + lane / CPR;
                 const int key = min(key0 + row, S - 1);
                 const int ck = (lane % CPR) ^ (row & KSW);
-                const int cv = (lane % CPR) ^ ((row & VSW) << 1);
+                const int cv = (lane % CPR) ^ vswz(row);
                 dma16(kb + (int64_t)key * kvrs + 8 * ck, stg + blk * RPI * D);
                 dma16(vb + (int64_t)key * kvrs + 8 * cv, stg + TB + blk * RPI * D);
             }
@@ -246,7 +249,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
     for (int db = 0; db < NDB; ++db) {
         const int R1 = 32 * kgrp_ + 4 * h + j16 / 4;
         const int ch = 4 * db + 2 * blk2 + ((j16 & 3) >> 1);
-        vro[db] = R1 * D + 8 * (ch ^ ((R1 & VSW) << 1)) + 4 * (j16 & 1);
+        vro[db] = R1 * D + 8 * (ch ^ vswz(R1)) + 4 * (j16 & 1);
     }
 
     for (int pass = 0; pass < 2; ++pass) {
