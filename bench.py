@@ -248,7 +248,9 @@ def run_config3(torch, kvhp, args):
     b, hq, hkv, d = c["b"], c["hq"], c["hkv"], c["d"]
     L1 = c["lens"] + 1
     max_len = int(L1.max())
-    splits = args.splits or kvhp.decode_auto_splits(b, hkv, d, max_len)
+    # 0 = the library's automatic split choice (per-sequence chunks balanced
+    # over the batch on the device, within decode_auto_splits slots)
+    splits = args.splits
     ws_bytes = kvhp.decode_workspace_bytes(b, hq, hkv, d, max_len, splits)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device="cuda")
     kvhp.decode_workspace_init(ws)
@@ -308,7 +310,8 @@ def run_config3(torch, kvhp, args):
         "step_us_median": float(np.median(step_us)),
         "decode_bytes": dbytes,
         "step_bytes": step_bytes,
-        "splits": splits,
+        "splits": splits if splits else
+                  f"auto (balanced, {kvhp.decode_auto_splits(b, hkv, d, max_len)} slots)",
         "sum_L": int(L1.sum()),
         "c": c,
     }

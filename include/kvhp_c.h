@@ -97,7 +97,11 @@ int kvhp_paged_gather_kv(const void* pool_k, const void* pool_v,
                          int head_dim, int num_pages, int max_len, void* out_k,
                          void* out_v, void* stream);
 
-/* Split count the decode entry points choose when num_splits == 0. */
+/* Split slots per sequence the decode entry points use when num_splits == 0
+ * (the workspace holds this many partials per (sequence, query head)).  For
+ * 8 or more sequences the auto mode cuts each sequence into its own number
+ * of splits, at most this many, chosen on the device from the lengths so
+ * that the batch fills the GPU's resident waves about once. */
 int kvhp_decode_auto_splits(int batch, int num_kv_heads, int head_dim,
                             int max_seq_len);
 /* Bytes of workspace kvhp_decode_attention needs for these arguments
@@ -118,7 +122,8 @@ int kvhp_decode_workspace_init(void* workspace, size_t workspace_bytes,
  *   q [batch][Hq][D] fp16, seq_lens device int32[batch] (keys 0..len-1),
  *   out [batch][Hq][D] fp16, kv_head = q_head / (Hq/Hkv),
  *   scale 1/sqrt(D) (decode_attention_split.cu:197).
- * num_splits: 0 = auto, else the number of KV chunks max_seq_len is cut into.
+ * num_splits: 0 = auto (see kvhp_decode_auto_splits), else the number of
+ * equal KV chunks max_seq_len is cut into.
  * workspace: NULL = library-owned per-device buffer (allocated on first use,
  * so not capturable into a HIP graph); otherwise at least
  * kvhp_decode_workspace_bytes() bytes.  With more than one split the call is

@@ -155,8 +155,11 @@ def _paged_case(rng, b, lens, hq, hkv, d, with_append, fused=False):
 
 
 @pytest.mark.parametrize("b,maxlen,hq,hkv,d", [(8, 1500, 32, 8, 128), (5, 300, 14, 2, 64),
-                                               (3, 900, 32, 4, 64), (4, 200, 16, 1, 128)])
+                                               (3, 900, 32, 4, 64), (4, 200, 16, 1, 128),
+                                               (80, 3000, 32, 8, 128), (70, 900, 32, 4, 64)])
 def test_paged_decode_with_append(b, maxlen, hq, hkv, d):
+    """Ragged paged batches (lengths from 0); batches of 8 or more run the
+    balanced split list (above 64 sequences its scan takes two passes)."""
     rng = np.random.default_rng(b * 31 + maxlen)
     lens = rng.integers(0, maxlen, size=b)
     note(f"paged decode B={b} Hq={hq} Hkv={hkv} D={d} lens={lens.tolist()}")
@@ -289,25 +292,31 @@ def test_decode_caller_workspace_reuse_and_empty_sequences():
         assert np.all(got[np.array(lens) == 0] == 0)
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (32, 4, 64), (12, 4, 96)])
-def test_paged_append_decode_matches_separate_calls(hq, hkv, d):
+@pytest.mark.parametrize("hq,hkv,d,tiles", [(32, 8, 128, 1), (32, 4, 64, 1), (12, 4, 96, 1),
+                                            (32, 8, 128, 10), (32, 4, 64, 10)])
+def test_paged_append_decode_matches_separate_calls(hq, hkv, d, tiles):
     """kvhp_paged_append_decode (one call: the covering split writes the new
     row into its page and attends it from registers) against
     kvhp_paged_append_kv followed by kvhp_decode_attention, bit for bit on
     both the pools and the outputs.  Ragged batch: an empty sequence, rows
     on page boundaries, a new position past the attended length (written,
-    not attended), and a new position on an unallocated page (dropped).
-    D=96 runs the fallback (append kernel, then the generic decode)."""
+    not attended), and a new position on an unallocated page (dropped; no
+    attended key lies on an unallocated page, whose reads would alias
+    physical page 0 while other sequences write their rows).
+    D=96 runs the fallback (append kernel, then the generic decode).  The
+    pattern tiled 10 times (70 sequences) runs the balanced split list."""
     import torch
-    rng = np.random.default_rng(500 + d)
-    lens = np.array([1000, 0, 1, 15, 16, 300, 2047], np.int32)   # cached tokens
+    rng = np.random.default_rng(500 + d + tiles)
+    lens = np.tile(np.array([1000, 0, 1, 15, 16, 300, 2047], np.int32), tiles)  # cached tokens
     b = lens.size
     bt, P = make_block_tables(rng, lens + 8)
     pos = lens.copy()
     seq = lens + 1
-    pos[5] = lens[5] + 4          # written, beyond the attended keys
-    seq[5] = lens[5]
-    bt[3, pos[3] // 16] = -1      # no page for this row: the write is dropped
+    pos[5::7] = lens[5::7] + 4    # written, beyond the attended keys
+    seq[5::7] = lens[5::7]
+    for i in range(4, b, 7):      # row 16 starts a page that has no id: the write is
+        bt[i, pos[i] // 16] = -1  # dropped, and the 16 attended keys stay on page 0
+        seq[i] = lens[i]
     pool_k = to_gpu_f16(oracle.normal_f16(rng, (hkv, P, 16, d)))
     pool_v = to_gpu_f16(oracle.normal_f16(rng, (hkv, P, 16, d)))
     k_new = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, d)))
