@@ -207,6 +207,8 @@ public:
     }
     void set_seq_len(int slot, int len) {
         check_slot(slot);
+        if (len < 0)
+            throw std::invalid_argument("PagedKVCache::set_seq_len: negative length");
         reserve(slot, len);
         lens_[slot] = len;
     }
@@ -221,6 +223,7 @@ public:
     // and its write position becomes the new length - 1.  Inactive slots get
     // length 0 and write position -1 (their appends are dropped).
     void begin_decode_step(int batch) {
+        check_batch(batch);
         for (int s = 0; s < batch; ++s) {
             if (!active_[s]) {
                 pos_[s] = -1;
@@ -234,6 +237,9 @@ public:
     // Write positions for a prefill of `num_tokens` tokens starting at each
     // slot's current length; lengths grow by num_tokens.
     void begin_prefill(int batch, int num_tokens) {
+        check_batch(batch);
+        if (num_tokens < 0)
+            throw std::invalid_argument("PagedKVCache::begin_prefill: negative token count");
         for (int s = 0; s < batch; ++s) {
             if (!active_[s]) {
                 pos_[s] = -1;
@@ -262,6 +268,8 @@ public:
     // Appends src [batch][num_tokens][Hkv][D] at each slot's write position.
     void append(int layer, const half* src_k, const half* src_v, int batch, int num_tokens,
                 Stream stream = nullptr) {
+        check_layer(layer);
+        check_batch(batch);
         hip::paged_append_kv(src_k, src_v, get_layer_ptr(layer, 0), get_layer_ptr(layer, 1),
                              block_tables(), max_pages_, write_positions(), batch, num_tokens,
                              num_kv_heads_, head_dim_, num_pages_, stream);
@@ -269,6 +277,8 @@ public:
     // Decode attention of q [batch][Hq][D] over each slot's seq_len keys.
     void decode(int layer, const half* q, half* out, int batch, int num_q_heads, int max_seq_len,
                 Stream stream = nullptr) const {
+        check_layer(layer);
+        check_batch(batch);
         hip::decode_gqa_split(q, k_view(layer), v_view(layer), seq_lens(), out, batch,
                               num_q_heads, num_kv_heads_, head_dim_, max_seq_len, nullptr, stream);
     }
@@ -278,6 +288,8 @@ public:
     // in one call (append and decode of the same step, fused).
     void append_decode(int layer, const half* k_new, const half* v_new, const half* q, half* out,
                        int batch, int num_q_heads, int max_seq_len, Stream stream = nullptr) {
+        check_layer(layer);
+        check_batch(batch);
         hip::paged_append_decode(q, k_new, v_new, k_view(layer), v_view(layer),
                                  write_positions(), seq_lens(), out, batch, num_q_heads,
                                  num_kv_heads_, head_dim_, max_seq_len, stream);
@@ -303,6 +315,16 @@ private:
     void check_slot(int slot) const {
         if (slot < 0 || slot >= max_batch_)
             throw std::out_of_range("PagedKVCache: slot " + std::to_string(slot));
+    }
+    // Device tables, lengths and write positions hold max_batch rows.
+    void check_batch(int batch) const {
+        if (batch < 0 || batch > max_batch_)
+            throw std::out_of_range("PagedKVCache: batch " + std::to_string(batch) +
+                                    " outside 0.." + std::to_string(max_batch_));
+    }
+    void check_layer(int layer) const {
+        if (layer < 0 || layer >= num_layers_)
+            throw std::out_of_range("PagedKVCache: layer " + std::to_string(layer));
     }
     void release_staging() {
         if (staged_) {

@@ -491,6 +491,35 @@ void case_paged_serving_steps() {
     EXPECT(same, "gathered K differs from the appended history");
 }
 
+void case_paged_cache_rejects() {
+    // Host-side contract of PagedKVCache: out-of-range batches, layers and
+    // slots, negative lengths, page exhaustion and a full batch all throw
+    // before any device work.
+    PagedKVCache cache(2, 2, 64, 4, 2, 3);   // 4 pages, 2 slots, 3 pages per sequence
+    auto throws = [](auto&& f) {
+        try {
+            f();
+        } catch (const std::exception&) {
+            return true;
+        }
+        return false;
+    };
+    half dummy[8] = {};
+    EXPECT(throws([&] { cache.begin_decode_step(3); }), "batch 3 of 2 accepted");
+    EXPECT(throws([&] { cache.begin_prefill(-1, 4); }), "negative batch accepted");
+    EXPECT(throws([&] { cache.begin_prefill(1, -4); }), "negative token count accepted");
+    EXPECT(throws([&] { cache.set_seq_len(0, -1); }), "negative length accepted");
+    EXPECT(throws([&] { cache.set_seq_len(2, 1); }), "slot 2 of 2 accepted");
+    EXPECT(throws([&] { cache.decode(2, dummy, dummy, 1, 4, 16); }), "layer 2 of 2 accepted");
+    EXPECT(throws([&] { cache.append(0, dummy, dummy, 3, 1); }), "append batch 3 accepted");
+    EXPECT(throws([&] { cache.reserve(0, 4 * 16); }), "more pages than max_pages_per_seq");
+    EXPECT(cache.add_sequence() == 0 && cache.add_sequence() == 1, "slots");
+    EXPECT(throws([&] { cache.add_sequence(); }), "third sequence in a batch of 2");
+    cache.reserve(0, 3 * 16);
+    EXPECT(throws([&] { cache.reserve(1, 2 * 16); }), "reserved past the pool (4 pages)");
+    EXPECT(cache.free_page_count() == 1, "a failed reserve took pages");
+}
+
 struct Case {
     const char* name;
     bool gpu;
@@ -517,6 +546,7 @@ int main(int argc, char** argv) {
         {"causal_gqa", true, case_causal_gqa},
         {"paged_identity_equals_kvcache", true, case_paged_identity_equals_kvcache},
         {"paged_serving_steps", true, case_paged_serving_steps},
+        {"paged_cache_rejects", true, case_paged_cache_rejects},
     };
     for (const Case& c : cases) {
         if (c.gpu && !gpu) continue;
