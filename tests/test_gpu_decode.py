@@ -167,6 +167,33 @@ def test_paged_decode_with_append(b, maxlen, hq, hkv, d):
     assert_attn_close(got, ref, "paged")
 
 
+@pytest.mark.parametrize("case", ["one_long", "many_short", "all_empty_but_one", "mixed_300"])
+def test_balanced_split_list_corners(case):
+    """The automatic split mode for batches of 8 or more balances on the
+    device; its corners: one long sequence among near-empty ones (its split
+    count reaches the plan's slots), 300 short sequences (fewer wave slots
+    per sequence than sequences), eleven sequences holding only the appended
+    token beside one long one, and 300 mixed lengths (cached lengths of 0
+    included).  Paged, D=64, against the oracle."""
+    rng = np.random.default_rng({"one_long": 11, "many_short": 12, "all_empty_but_one": 13,
+                                 "mixed_300": 14}[case])
+    hq, hkv, d = 16, 4, 64
+    if case == "one_long":
+        lens = np.array([6000] + [1] * 8)
+    elif case == "many_short":
+        lens = rng.integers(1, 40, size=300)
+    elif case == "all_empty_but_one":
+        lens = np.array([0] * 11 + [2500])
+    else:
+        lens = rng.integers(0, 700, size=300)
+        lens[::7] = 0
+    lens = lens.astype(np.int32)
+    note(f"balanced corner {case}: B={lens.size} max={int(lens.max())} sum={int(lens.sum())}")
+    got, ref = _paged_case(rng, lens.size, lens, hq, hkv, d, with_append=True,
+                           fused=case != "many_short")
+    assert_attn_close(got, ref, case)
+
+
 @pytest.mark.parametrize("fused", [False, True])
 def test_config3_paged_decode_full_size(fused):
     """BASELINE config 3 at full size: 32 sequences with seeded lengths in
