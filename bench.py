@@ -547,7 +547,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
         if args.profile == "prefill":
-            r4 = run_config4(torch, kvhp, sizes=(2048,), reps=args.steps)
+            # S=2048 runs the key-split kernel, S=8192 the ping-pong one
+            r4 = run_config4(torch, kvhp, sizes=(2048, 8192), reps=args.steps)
             print(json.dumps({"profile": "prefill", "config4": r4}))
             return
         if args.profile == "c5":
