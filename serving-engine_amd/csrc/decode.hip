@@ -830,7 +830,10 @@ void launch_fast(const DecodeArgs& args, dim3 grid, bool paged, hipStream_t s) {
             // at most max(balance, B * cap / max_chunk) + B.
             const long long worst = ((long long)a.batch * a.cap + a.max_chunk - 1) / a.max_chunk;
             const long long units = std::max<long long>(a.balance, worst) + a.batch;
-            grid = dim3(a.Hkv, static_cast<unsigned>(units), 1);
+            if (units <= 65535)   // grid y limit; beyond it the fixed chunk serves
+                grid = dim3(a.Hkv, static_cast<unsigned>(units), 1);
+            else
+                a.balance = 0;
         }
     }
     if (paged)
