@@ -13,6 +13,12 @@
 // int32 seq_lens [max_batch], with a host free list of pages.  Under the
 // identity block table one sequence's pool is byte-identical to KVCache's
 // [num_kv_heads][max_seq][head_dim] block for max_seq = 16 * num_pages.
+// Pages carry reference counts: share_prefix() lets a sequence reuse another's
+// full prefix pages (the runner contract's prefix sharing,
+// docs/runner_interface.md:30-33); a decode write into a shared page throws,
+// as the reference runner asserts (:51), and prefill writes go through a
+// write table in which shared pages are -1, so they are never overwritten
+// ("share" mode, :33).
 #pragma once
 
 #include <algorithm>
@@ -133,8 +139,8 @@ public:
         pool_.allocate((size_t)num_layers * 2 * num_kv_heads * num_pages * kPage * head_dim);
         pool_.zero();
         // one device block: tables [max_batch][max_pages], seq_lens [max_batch],
-        // write positions [max_batch]
-        meta_words_ = (size_t)max_batch * max_pages_per_seq + 2 * (size_t)max_batch;
+        // write positions [max_batch], write tables [max_batch][max_pages]
+        meta_words_ = 2 * (size_t)max_batch * max_pages_per_seq + 2 * (size_t)max_batch;
         meta_.allocate(meta_words_);
         void* p = nullptr;
         HIP_CHECK(hipHostMalloc(&p, meta_words_ * sizeof(int32_t), hipHostMallocDefault));
@@ -147,8 +153,10 @@ public:
         active_.assign(max_batch, false);
         free_pages_.resize(num_pages);
         for (int i = 0; i < num_pages; ++i) free_pages_[i] = num_pages - 1 - i;  // pop 0 first
+        refs_.assign(num_pages, 0);
         std::copy(tables_.begin(), tables_.end(), staging_);
         std::fill(staging_ + tables_.size(), staging_ + meta_words_, 0);
+        std::fill(staging_ + tables_.size() + 2 * (size_t)max_batch, staging_ + meta_words_, -1);
         HIP_CHECK(hipMemcpy(meta_.data(), staging_, meta_words_ * sizeof(int32_t),
                             hipMemcpyHostToDevice));
     }
@@ -162,6 +170,9 @@ public:
     const int32_t* block_tables() const { return meta_.data(); }
     const int32_t* seq_lens() const { return meta_.data() + (size_t)max_batch_ * max_pages_; }
     const int32_t* write_positions() const { return seq_lens() + max_batch_; }
+    // Block tables for writes: as block_tables(), with pages that more than
+    // one sequence holds set to -1 (writes there are dropped).
+    const int32_t* write_block_tables() const { return write_positions() + max_batch_; }
     hip::KVView k_view(int layer) const { return view(layer, 0); }
     hip::KVView v_view(int layer) const { return view(layer, 1); }
 
@@ -187,8 +198,10 @@ public:
         if (need - pages_used_[slot] > (int)free_pages_.size())
             throw std::runtime_error("PagedKVCache::reserve: out of pages");
         while (pages_used_[slot] < need) {
-            tables_[(size_t)slot * max_pages_ + pages_used_[slot]] = free_pages_.back();
+            const int32_t page = free_pages_.back();
             free_pages_.pop_back();
+            refs_[page] = 1;
+            tables_[(size_t)slot * max_pages_ + pages_used_[slot]] = page;
             ++pages_used_[slot];
         }
     }
@@ -197,7 +210,7 @@ public:
         check_slot(slot);
         for (int i = 0; i < pages_used_[slot]; ++i) {
             int32_t& e = tables_[(size_t)slot * max_pages_ + i];
-            free_pages_.push_back(e);
+            if (--refs_[e] == 0) free_pages_.push_back(e);
             e = -1;
         }
         pages_used_[slot] = 0;
@@ -212,6 +225,31 @@ public:
         reserve(slot, len);
         lens_[slot] = len;
     }
+    // Prefix sharing: `dst` (an active slot holding no pages) takes the
+    // full pages covering the first num_tokens positions of `src` (a partial
+    // last page is never shared, so later writes stay private) and starts
+    // with that many cached tokens.  Returns the shared token count.
+    int share_prefix(int dst, int src, int num_tokens) {
+        check_slot(dst);
+        check_slot(src);
+        if (dst == src || !active_[dst] || !active_[src])
+            throw std::invalid_argument("PagedKVCache::share_prefix: two distinct active slots needed");
+        if (pages_used_[dst] != 0)
+            throw std::logic_error("PagedKVCache::share_prefix: destination already holds pages");
+        if (num_tokens < 0 || num_tokens > lens_[src])
+            throw std::out_of_range("PagedKVCache::share_prefix: prefix longer than the source");
+        const int n = num_tokens / kPage;
+        for (int i = 0; i < n; ++i) {
+            const int32_t page = tables_[(size_t)src * max_pages_ + i];
+            tables_[(size_t)dst * max_pages_ + i] = page;
+            ++refs_[page];
+        }
+        pages_used_[dst] = n;
+        lens_[dst] = n * kPage;
+        return n * kPage;
+    }
+    // Sequences holding physical page `page` (0: free).
+    int page_refs(int page) const { return refs_.at(page); }
     int seq_len(int slot) const { return lens_.at(slot); }
     int pages_used(int slot) const { return pages_used_.at(slot); }
     int free_page_count() const { return (int)free_pages_.size(); }
@@ -221,9 +259,27 @@ public:
     // num_tokens - 1" (docs/runner_interface.md:37-53): every active slot's
     // length grows by one, a page is added when it crosses a page boundary,
     // and its write position becomes the new length - 1.  Inactive slots get
-    // length 0 and write position -1 (their appends are dropped).
+    // length 0 and write position -1 (their appends are dropped).  A write
+    // into a page that another sequence also holds throws, as the reference
+    // runner asserts (docs/runner_interface.md:51); so does a step the free
+    // pages cannot cover.  Either check runs before any slot changes.
     void begin_decode_step(int batch) {
         check_batch(batch);
+        int new_pages = 0;
+        for (int s = 0; s < batch; ++s) {
+            if (!active_[s]) continue;
+            const int idx = lens_[s] / kPage;   // page of the write position
+            if (idx >= max_pages_)
+                throw std::runtime_error("PagedKVCache::begin_decode_step: slot " + std::to_string(s) +
+                                         " exceeds max_pages_per_seq");
+            if (idx >= pages_used_[s])
+                new_pages += idx + 1 - pages_used_[s];
+            else if (refs_[tables_[(size_t)s * max_pages_ + idx]] > 1)
+                throw std::logic_error("PagedKVCache::begin_decode_step: slot " + std::to_string(s) +
+                                       " would write into a shared page");
+        }
+        if (new_pages > (int)free_pages_.size())
+            throw std::runtime_error("PagedKVCache::begin_decode_step: out of pages");
         for (int s = 0; s < batch; ++s) {
             if (!active_[s]) {
                 pos_[s] = -1;
@@ -235,7 +291,8 @@ public:
         }
     }
     // Write positions for a prefill of `num_tokens` tokens starting at each
-    // slot's current length; lengths grow by num_tokens.
+    // slot's current length; lengths grow by num_tokens.  Writes go through
+    // write_block_tables(), so positions on shared pages are left as cached.
     void begin_prefill(int batch, int num_tokens) {
         check_batch(batch);
         if (num_tokens < 0)
@@ -259,6 +316,9 @@ public:
         std::copy(tables_.begin(), tables_.end(), staging_);
         std::copy(lens_.begin(), lens_.end(), staging_ + tables_.size());
         std::copy(pos_.begin(), pos_.end(), staging_ + tables_.size() + max_batch_);
+        int32_t* wt = staging_ + tables_.size() + 2 * (size_t)max_batch_;
+        for (size_t i = 0; i < tables_.size(); ++i)
+            wt[i] = tables_[i] >= 0 && refs_[tables_[i]] > 1 ? -1 : tables_[i];
         HIP_CHECK(hipMemcpyAsync(meta_.data(), staging_, meta_words_ * sizeof(int32_t),
                                  hipMemcpyHostToDevice, stream));
         HIP_CHECK(hipEventRecord(staged_, stream));
@@ -271,8 +331,8 @@ public:
         check_layer(layer);
         check_batch(batch);
         hip::paged_append_kv(src_k, src_v, get_layer_ptr(layer, 0), get_layer_ptr(layer, 1),
-                             block_tables(), max_pages_, write_positions(), batch, num_tokens,
-                             num_kv_heads_, head_dim_, num_pages_, stream);
+                             write_block_tables(), max_pages_, write_positions(), batch,
+                             num_tokens, num_kv_heads_, head_dim_, num_pages_, stream);
     }
     // Decode attention of q [batch][Hq][D] over each slot's seq_len keys.
     void decode(int layer, const half* q, half* out, int batch, int num_q_heads, int max_seq_len,
@@ -349,6 +409,7 @@ private:
     std::vector<int> pages_used_;
     std::vector<bool> active_;
     std::vector<int32_t> free_pages_;
+    std::vector<int> refs_;
 };
 
 }  // namespace engine

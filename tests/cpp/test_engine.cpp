@@ -520,6 +520,160 @@ void case_paged_cache_rejects() {
     EXPECT(cache.free_page_count() == 1, "a failed reserve took pages");
 }
 
+void case_paged_prefix_sharing() {
+    // Prefix sharing (docs/runner_interface.md:30-33, 51): sequence B shares
+    // A's two full prompt pages, recomputes its whole prompt in "share" mode
+    // with K/V that differ on the shared part, and the prefill's page writes
+    // through write_block_tables() leave A's pages untouched.  Decode steps
+    // then write only private pages; a decode write into a shared page
+    // throws before any slot changes; pages return to the free list when the
+    // last holder releases them.
+    std::mt19937 rng(2207);
+    const int hq = 4, hkv = 2, d = 64, SA = 40, SB = 45;
+    PagedKVCache cache(1, hkv, d, 16, 3, 8);
+    const int mp = cache.max_pages_per_seq();
+    auto gather = [&](int slot, int len) {
+        DeviceBuffer<half> gk((size_t)hkv * len * d), gv(gk.size());
+        std::vector<int32_t> l1 = {len};
+        DeviceBuffer<int32_t> dl = upload(l1);
+        hip::paged_gather_kv(cache.get_layer_ptr(0, 0), cache.get_layer_ptr(0, 1),
+                             cache.block_tables() + (size_t)slot * mp, mp, dl.data(), 1, hkv, d,
+                             cache.num_pages(), len, gk.data(), gv.data());
+        HIP_CHECK(hipDeviceSynchronize());
+        return std::make_pair(download(gk), download(gv));
+    };
+    // token-major [T][hkv][d] -> head-major [hkv][T][d]
+    auto head_major = [&](const std::vector<half>& x, int T) {
+        std::vector<half> y(x.size());
+        for (int t = 0; t < T; ++t)
+            for (int h = 0; h < hkv; ++h)
+                std::memcpy(&y[((size_t)h * T + t) * d], &x[((size_t)t * hkv + h) * d], d * 2);
+        return y;
+    };
+    auto prefill = [&](int slot, int S, const std::vector<half>& k, const std::vector<half>& v) {
+        auto q = random_half(rng, (size_t)S * hq * d, -1, 1);
+        auto dq = upload(q), dk = upload(k), dv = upload(v);
+        DeviceBuffer<half> out(q.size());
+        hip::flash_prefill_gqa_paged(dq.data(), dk.data(), dv.data(), out.data(), S, hq, hkv, d, 1,
+                                     cache.get_layer_ptr(0, 0), cache.get_layer_ptr(0, 1),
+                                     cache.write_block_tables() + (size_t)slot * mp, mp,
+                                     cache.num_pages());
+        HIP_CHECK(hipDeviceSynchronize());
+        std::vector<float> ref(q.size());
+        kvo_causal_gqa_rows(to_float(q).data(), to_float(k).data(), to_float(v).data(), ref.data(), S,
+                            hq, hkv, d, 0, S, 4);
+        check_close(download(out), ref, "prefill");
+    };
+
+    const int a = cache.add_sequence();
+    auto ka = random_half(rng, (size_t)SA * hkv * d, -1, 1), va = random_half(rng, ka.size(), -1, 1);
+    cache.set_seq_len(a, SA);
+    cache.sync();
+    prefill(a, SA, ka, va);
+
+    const int b = cache.add_sequence();
+    EXPECT(cache.share_prefix(b, a, SA) == 32, "shared token count");
+    EXPECT(cache.seq_len(b) == 32 && cache.pages_used(b) == 2, "B after share: %d tokens, %d pages",
+           cache.seq_len(b), cache.pages_used(b));
+    for (int i = 0; i < 2; ++i) {
+        EXPECT(cache.host_block_table(b)[i] == cache.host_block_table(a)[i], "page %d not shared", i);
+        EXPECT(cache.page_refs(cache.host_block_table(a)[i]) == 2, "refs of shared page %d", i);
+    }
+    EXPECT(cache.page_refs(cache.host_block_table(a)[2]) == 1, "A's partial page shared");
+    // "share" mode: B recomputes all 45 prompt tokens; its K/V on the shared
+    // 32 differ from A's, so any write into a shared page would show.
+    auto kb = random_half(rng, (size_t)SB * hkv * d, -1, 1), vb = random_half(rng, kb.size(), -1, 1);
+    cache.set_seq_len(b, SB);
+    cache.sync();
+    prefill(b, SB, kb, vb);
+    auto ga = gather(a, SA);
+    EXPECT(bits_equal(ga.first, head_major(ka, SA)) && bits_equal(ga.second, head_major(va, SA)),
+           "A's pages changed by B's prefill");
+    // B's cache: A's K/V on the shared pages, its own after them
+    std::vector<half> hb_k(kb), hb_v(vb);
+    std::copy(ka.begin(), ka.begin() + (size_t)32 * hkv * d, hb_k.begin());
+    std::copy(va.begin(), va.begin() + (size_t)32 * hkv * d, hb_v.begin());
+    auto gb = gather(b, SB);
+    EXPECT(bits_equal(gb.first, head_major(hb_k, SB)) && bits_equal(gb.second, head_major(hb_v, SB)),
+           "B's cache is not A's shared prefix + B's own suffix");
+
+    // two decode steps for both: writes land on private pages only
+    std::vector<half> hist_k[2] = {ka, hb_k}, hist_v[2] = {va, hb_v};
+    for (int st = 0; st < 2; ++st) {
+        cache.begin_decode_step(2);
+        cache.sync();
+        auto q = random_half(rng, (size_t)2 * hq * d, -1, 1);
+        auto kn = random_half(rng, (size_t)2 * hkv * d, -1, 1), vn = random_half(rng, kn.size(), -1, 1);
+        auto dq = upload(q), dk = upload(kn), dv = upload(vn);
+        DeviceBuffer<half> out(q.size());
+        const int max_len = std::max(cache.seq_len(a), cache.seq_len(b));
+        cache.append_decode(0, dk.data(), dv.data(), dq.data(), out.data(), 2, hq, max_len);
+        HIP_CHECK(hipDeviceSynchronize());
+        std::vector<float> kc((size_t)2 * hkv * max_len * d, 0.f), vc(kc.size(), 0.f);
+        std::vector<int32_t> lens = {cache.seq_len(a), cache.seq_len(b)};
+        for (int s = 0; s < 2; ++s) {
+            hist_k[s].insert(hist_k[s].end(), kn.begin() + (size_t)s * hkv * d, kn.begin() + (size_t)(s + 1) * hkv * d);
+            hist_v[s].insert(hist_v[s].end(), vn.begin() + (size_t)s * hkv * d, vn.begin() + (size_t)(s + 1) * hkv * d);
+            for (int t = 0; t < lens[s]; ++t)
+                for (int h = 0; h < hkv; ++h)
+                    for (int i = 0; i < d; ++i) {
+                        kc[(((size_t)s * hkv + h) * max_len + t) * d + i] = half_to_float(hist_k[s][((size_t)t * hkv + h) * d + i]);
+                        vc[(((size_t)s * hkv + h) * max_len + t) * d + i] = half_to_float(hist_v[s][((size_t)t * hkv + h) * d + i]);
+                    }
+        }
+        std::vector<float> ref(q.size());
+        kvo_decode_attention(to_float(q).data(), kc.data(), vc.data(), lens.data(), ref.data(), 2, hq,
+                             hkv, d, max_len, 4);
+        check_close(download(out), ref, "decode over a shared prefix");
+    }
+    ga = gather(a, SA + 2);
+    gb = gather(b, SB + 2);
+    EXPECT(bits_equal(ga.first, head_major(hist_k[0], SA + 2)), "A's history after decode");
+    EXPECT(bits_equal(gb.first, head_major(hist_k[1], SB + 2)) &&
+               bits_equal(gb.second, head_major(hist_v[1], SB + 2)),
+           "B's history after decode");
+
+    // C shares B's prefix, then is cut back into a shared page: its decode
+    // write would mutate a shared page, so the step throws and changes nothing
+    const int c = cache.add_sequence();
+    EXPECT(cache.share_prefix(c, b, 40) == 32, "C's shared count");
+    cache.set_seq_len(c, 20);
+    const int len_a = cache.seq_len(a), free_before = cache.free_page_count();
+    bool threw = false;
+    try {
+        cache.begin_decode_step(3);
+    } catch (const std::logic_error&) {
+        threw = true;
+    }
+    EXPECT(threw, "decode write into a shared page accepted");
+    EXPECT(cache.seq_len(a) == len_a && cache.seq_len(c) == 20 && cache.free_page_count() == free_before,
+           "a rejected step changed the cache");
+    EXPECT(cache.page_refs(cache.host_block_table(b)[0]) == 3, "refs with three holders");
+
+    // release: a page is freed only by its last holder
+    const int shared0 = cache.host_block_table(a)[0];
+    const int priv_a = cache.pages_used(a) - 2;
+    cache.release(a);
+    EXPECT(cache.free_page_count() == free_before + priv_a, "A's release freed %d pages, expected %d",
+           cache.free_page_count() - free_before, priv_a);
+    EXPECT(cache.page_refs(shared0) == 2, "refs after A's release");
+    cache.release(c);
+    EXPECT(cache.page_refs(shared0) == 1 && cache.free_page_count() == free_before + priv_a,
+           "C's release freed pages B still holds");
+    cache.release(b);
+    EXPECT(cache.page_refs(shared0) == 0 && cache.free_page_count() == cache.num_pages(),
+           "every page free after the last release");
+    EXPECT(cache.add_sequence() == 0, "slot reuse after release");
+    EXPECT(cache.add_sequence() == 1, "slot reuse after release");
+    bool bad_share = false;
+    try {
+        cache.share_prefix(1, 0, 16);   // source holds 0 tokens
+    } catch (const std::out_of_range&) {
+        bad_share = true;
+    }
+    EXPECT(bad_share, "prefix longer than the source accepted");
+}
+
 struct Case {
     const char* name;
     bool gpu;
@@ -547,6 +701,7 @@ int main(int argc, char** argv) {
         {"paged_identity_equals_kvcache", true, case_paged_identity_equals_kvcache},
         {"paged_serving_steps", true, case_paged_serving_steps},
         {"paged_cache_rejects", true, case_paged_cache_rejects},
+        {"paged_prefix_sharing", true, case_paged_prefix_sharing},
     };
     for (const Case& c : cases) {
         if (c.gpu && !gpu) continue;
