@@ -233,6 +233,13 @@ int kvhp_apply_rope(void* q, void* k, int64_t seq_len, int64_t num_q_heads, int6
 int kvhp_split_qkv_rope(const void* qkv, int64_t seq_len, int num_q_heads, int num_kv_heads,
                         int head_dim, int64_t start_pos, float rope_theta, void* q, void* k,
                         void* v, void* stream);
+/* Batched decode helper: as kvhp_split_qkv_rope for `rows` sequences, row r
+ * rotated at positions[r] (device int32; negative = idle row, rotated as
+ * position 0) -- the reference's per-token rope (rope.cu:8-57) at each
+ * sequence's write position. */
+int kvhp_split_qkv_rope_rows(const void* qkv, int64_t rows, int num_q_heads, int num_kv_heads,
+                             int head_dim, const int32_t* positions, float rope_theta, void* q,
+                             void* k, void* v, void* stream);
 /* Replaces engine::cuda::swiglu (kernels.h:150-158): out = silu(g) * u. */
 int kvhp_swiglu(const void* gate, const void* up, void* out, int64_t count, void* stream);
 /* swiglu over rows of a fused [gate | up] buffer [rows][2n] -> out [rows][n]. */
@@ -247,6 +254,9 @@ int kvhp_embedding(const int32_t* token_ids, const void* table, void* out, int64
  * ++*log_count; ++*seq_len (the next step's "bump"). */
 int kvhp_argmax(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, int32_t* log,
                 int32_t* log_count, void* stream);
+/* Batched greedy sampling: tokens[r] = argmax of row r of logits [rows][n]
+ * (same tie and NaN rules as kvhp_argmax); one workgroup per row. */
+int kvhp_argmax_rows(const float* logits, int64_t rows, int64_t n, int32_t* tokens, void* stream);
 /* Seeded N(0, std_dev) fp16 fill (synthetic weights): element i of stream
  * stream_id is a Box-Muller normal of two splitmix64 hashes of
  * (seed, stream_id, i). */
@@ -308,6 +318,39 @@ int kvhp_llama_generate(void* model, int n_steps, int use_graph, int32_t* tokens
                         float* elapsed_ms);
 /* Device pointer and element count of a model tensor (fp16). */
 int kvhp_llama_tensor(void* model, int layer, int which, void** ptr, size_t* count);
+
+/* ---- Batched serving over caller-owned pages: the reference runner
+ * contract (docs/runner_interface.md:18-53; Runner.prefill / decode_step)
+ * with the scheduler's page pool and block tables in the caller's hands.
+ * pool: [num_layers][2][Hkv][num_pages][16][D] fp16 (engine::PagedKVCache's
+ * raw_data() layout); block tables int32 rows of max_pages page ids (-1 =
+ * none: reads clamp, writes are dropped).  The model's activation buffers
+ * (max_ctx rows) are reused, so calls on one model must not overlap: issue
+ * them on one stream, or synchronise between streams. */
+
+/* prefill(seq) (runner_interface.md:20-33): the n prompt ids (host) run
+ * through the model; the K/V of position t go to page block_table[t/16]
+ * (device, one row) slot t%16 of every layer -- pass the write table
+ * (engine::PagedKVCache::write_block_tables) so pages shared with other
+ * sequences keep their cached K/V ("share" prefix mode).  The caller has
+ * allocated pages for all n positions (n <= 16 * max_pages, n <= max_ctx).
+ * logits_out (host, V floats, may be NULL) are those of the last position;
+ * *next_token its greedy argmax.  Runs on `stream`; returns when done. */
+int kvhp_llama_prefill_paged(void* model, const int32_t* tokens, int n, void* pool,
+                             int num_pages, const int32_t* block_table, int max_pages,
+                             float* logits_out, int32_t* next_token, void* stream);
+/* decode_step(seqs) (runner_interface.md:37-53) for `batch` sequences
+ * (batch <= max_ctx), all arguments device memory: row b embeds tokens[b],
+ * appends its K/V at positions[b] through row b of block_tables [batch]
+ * [max_pages] (-1: an idle row, nothing written), attends over seq_lens[b]
+ * keys (<= max_seq_len; the caller has already bumped it, so positions[b] =
+ * seq_lens[b] - 1), and ends in fp32 logits [batch][V] and greedy
+ * next_tokens[batch] (lowest index on ties).  Each projection is one
+ * batch-row GEMM.  Asynchronous on `stream`. */
+int kvhp_llama_decode_paged(void* model, const int32_t* tokens, int batch, void* pool,
+                            int num_pages, const int32_t* block_tables, int max_pages,
+                            const int32_t* positions, const int32_t* seq_lens, int max_seq_len,
+                            float* logits, int32_t* next_tokens, void* stream);
 
 #ifdef __cplusplus
 }

@@ -14,6 +14,14 @@
 // argmax on device) so that it can be captured once in a HIP graph and
 // replayed per token.
 //
+// Batched serving (kvhp_llama_prefill_paged / kvhp_llama_decode_paged) runs
+// the same layers over a caller-owned page pool [L][2][Hkv][P][16][D] (the
+// engine::PagedKVCache layout) and caller block tables, per the reference
+// runner contract (docs/runner_interface.md:18-53): the caller has already
+// allocated pages and bumped lengths; a decode step appends each sequence's
+// K/V at its write position and attends over its seq_len keys; B sequences
+// go through each projection as one B-row GEMM.
+//
 // Prefill projections are library GEMMs (rocBLAS, fp16 in, fp32 compute,
 // fp16 out; the o and down projections accumulate into the residual stream
 // with beta = 1); attention is the flash prefill kernel, which also writes
@@ -58,6 +66,7 @@ struct Model {
     f16* final_norm = nullptr; // [H]
     f16* lm_head = nullptr;    // [V][H]
     std::vector<Layer> layers;
+    f16* pool = nullptr;       // [L][2][Hkv][P][16][D], layer pools point into it
     int32_t* bt = nullptr;     // [P] identity page order
     // prefill activations, sized for max_ctx rows
     f16 *hidden = nullptr, *norm = nullptr, *qkv = nullptr, *q = nullptr, *k = nullptr,
@@ -66,7 +75,8 @@ struct Model {
     f16 *x = nullptr, *q1 = nullptr, *attn1 = nullptr, *act1 = nullptr;
     float* logits = nullptr;   // [V]
     int32_t* tokens = nullptr; // [max_ctx] prompt ids
-    int32_t* state = nullptr;  // [0] seq_len, [1] current token, [2] log count
+    int32_t* state = nullptr;  // [0] seq_len, [1] current token, [2] log count,
+                               // [3] token of a paged prefill
     int32_t* log = nullptr;    // [max_ctx] generated tokens
     void* ws = nullptr;        // decode attention workspace
     size_t ws_bytes = 0;
@@ -124,18 +134,108 @@ int linear(Model& m, const f16* A, const f16* W, f16* C, int M, int N, int K, bo
                       "linear");
 }
 
-kvhp_kv_view pool_view(const Model& m, const f16* pool) {
+// C[M][N] = A[M][K] W[N][K]^T with fp32 C (the batched LM head).
+int linear_f32(Model& m, const f16* A, const f16* W, float* C, int M, int N, int K) {
+    const float alpha = 1.f, beta = 0.f;
+    return blas_check(rocblas_gemm_ex(m.blas, rocblas_operation_transpose,
+                                      rocblas_operation_none, N, M, K, &alpha, W,
+                                      rocblas_datatype_f16_r, K, A, rocblas_datatype_f16_r, K,
+                                      &beta, C, rocblas_datatype_f32_r, N, C,
+                                      rocblas_datatype_f32_r, N, rocblas_datatype_f32_r,
+                                      rocblas_gemm_algo_standard, 0, 0),
+                      "linear_f32");
+}
+
+// K/V pages a forward writes and reads: pool [L][2][Hkv][num_pages][16][D]
+// and block-table rows of max_pages entries.
+struct Pages {
+    f16* base;
+    int num_pages;
+    const int32_t* bt;
+    int max_pages;
+};
+
+f16* layer_pool(const Model& m, const Pages& pg, int l, int is_v) {
+    return pg.base + (size_t)(2 * l + is_v) * m.c.num_kv_heads * pg.num_pages * kPage * m.c.head_dim;
+}
+
+kvhp_kv_view pages_view(const Model& m, const Pages& pg, int l, int is_v) {
     kvhp_kv_view v{};
-    v.data = pool;
+    v.data = layer_pool(m, pg, l, is_v);
     v.stride_b = 0;
-    v.stride_h = (int64_t)m.P * kPage * m.c.head_dim;
+    v.stride_h = (int64_t)pg.num_pages * kPage * m.c.head_dim;
     v.stride_s = m.c.head_dim;
     v.stride_d = 1;
-    v.block_table = m.bt;
-    v.max_pages = m.P;
+    v.block_table = pg.bt;
+    v.max_pages = pg.max_pages;
     v.page_size = kPage;
-    v.num_pages = m.P;
+    v.num_pages = pg.num_pages;
     return v;
+}
+
+Pages own_pages(const Model& m) { return Pages{m.pool, m.P, m.bt, m.P}; }
+
+// rocBLAS follows `s` for the lifetime of this object, then the model's
+// stream again.
+struct BlasOn {
+    Model& m;
+    BlasOn(Model& mm, hipStream_t s) : m(mm) { (void)rocblas_set_stream(m.blas, s); }
+    ~BlasOn() { (void)rocblas_set_stream(m.blas, m.stream); }
+};
+
+// Prompt forward of m.tokens[0, n) (one sequence): final hidden rows in
+// m.hidden, the K/V of every position written through pg.bt (ids -1, pages
+// held by other sequences, are skipped by the writes).
+int prefill_layers(Model& m, int n, const Pages& pg, void* s) {
+    const kvhp_llama_config& c = m.c;
+    const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
+    const int F = c.ffn_size, NQKV = (Hq + 2 * Hkv) * D;
+    KVHP_TRY(kvhp_embedding(m.tokens, m.embed, m.hidden, n, H, c.vocab_size, s));
+    for (int l = 0; l < c.num_layers; ++l) {
+        const Layer& L = m.layers[l];
+        KVHP_TRY(kvhp_rmsnorm(m.hidden, L.attn_norm, m.norm, n, H, c.rms_eps, s));
+        KVHP_TRY(linear(m, m.norm, L.w_qkv, m.qkv, n, NQKV, H, false));
+        KVHP_TRY(kvhp_split_qkv_rope(m.qkv, n, Hq, Hkv, D, 0, c.rope_theta, m.q, m.k, m.v, s));
+        KVHP_TRY(kvhp_flash_prefill_paged(m.q, m.k, m.v, m.attn, n, Hq, Hkv, D, 1,
+                                          layer_pool(m, pg, l, 0), layer_pool(m, pg, l, 1), pg.bt,
+                                          pg.max_pages, pg.num_pages, s));
+        KVHP_TRY(linear(m, m.attn, L.w_o, m.hidden, n, H, Hq * D, true));
+        KVHP_TRY(kvhp_rmsnorm(m.hidden, L.ffn_norm, m.norm, n, H, c.rms_eps, s));
+        KVHP_TRY(linear(m, m.norm, L.w_gate_up, m.gu, n, 2 * F, H, false));
+        KVHP_TRY(kvhp_swiglu_rows(m.gu, m.act, n, F, s));
+        KVHP_TRY(linear(m, m.act, L.w_down, m.hidden, n, H, F, true));
+    }
+    return KVHP_OK;
+}
+
+// One batched decode step: row b takes token tokens[b] at position
+// positions[b] (its K/V appended there through row b of pg.bt) and attends
+// over seq_lens[b] keys; fp32 logits [B][V], greedy tokens next[b].
+int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
+                const int32_t* positions, const int32_t* seq_lens, int max_seq_len,
+                float* logits, int32_t* next, void* s) {
+    const kvhp_llama_config& c = m.c;
+    const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
+    const int F = c.ffn_size, NQKV = (Hq + 2 * Hkv) * D;
+    KVHP_TRY(kvhp_embedding(tokens, m.embed, m.hidden, B, H, c.vocab_size, s));
+    for (int l = 0; l < c.num_layers; ++l) {
+        const Layer& L = m.layers[l];
+        KVHP_TRY(kvhp_rmsnorm(m.hidden, L.attn_norm, m.norm, B, H, c.rms_eps, s));
+        KVHP_TRY(linear(m, m.norm, L.w_qkv, m.qkv, B, NQKV, H, false));
+        KVHP_TRY(kvhp_split_qkv_rope_rows(m.qkv, B, Hq, Hkv, D, positions, c.rope_theta, m.q, m.k,
+                                          m.v, s));
+        const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
+        KVHP_TRY(kvhp_paged_append_decode(m.q, m.k, m.v, &kv, &vv, positions, seq_lens, m.attn, B,
+                                          Hq, Hkv, D, max_seq_len, 0, nullptr, 0, s));
+        KVHP_TRY(linear(m, m.attn, L.w_o, m.hidden, B, H, Hq * D, true));
+        KVHP_TRY(kvhp_rmsnorm(m.hidden, L.ffn_norm, m.norm, B, H, c.rms_eps, s));
+        KVHP_TRY(linear(m, m.norm, L.w_gate_up, m.gu, B, 2 * F, H, false));
+        KVHP_TRY(kvhp_swiglu_rows(m.gu, m.act, B, F, s));
+        KVHP_TRY(linear(m, m.act, L.w_down, m.hidden, B, H, F, true));
+    }
+    KVHP_TRY(kvhp_rmsnorm(m.hidden, m.final_norm, m.norm, B, H, c.rms_eps, s));
+    KVHP_TRY(linear_f32(m, m.norm, m.lm_head, logits, B, c.vocab_size, H));
+    return kvhp_argmax_rows(logits, B, c.vocab_size, next, s);
 }
 
 // One decode step on the device: token m.state[1] at position m.state[0] - 1.
@@ -152,7 +252,9 @@ int decode_step_kernels(Model& m, bool embed_token) {
         KVHP_TRY(kvhp_rmsnorm_qkv_rope_append(L.w_qkv, m.x, L.attn_norm, c.rms_eps, m.state,
                                               c.rope_theta, m.q1, L.pool_k, L.pool_v, m.bt, m.P,
                                               m.P, Hq, Hkv, D, H, s));
-        const kvhp_kv_view kv = pool_view(m, L.pool_k), vv = pool_view(m, L.pool_v);
+        const Pages pg = own_pages(m);
+        const int l = static_cast<int>(&L - m.layers.data());
+        const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
         KVHP_TRY(kvhp_decode_attention(m.q1, &kv, &vv, m.state, m.attn1, 1, Hq, Hkv, D, m.max_ctx,
                                        0, m.ws, m.ws_bytes, s));
         KVHP_TRY(kvhp_gemv_residual(L.w_o, m.attn1, m.x, m.x, H, Hq * D, s));
@@ -207,18 +309,22 @@ extern "C" int kvhp_llama_create(const kvhp_llama_config* cfg, uint64_t seed, in
     KVHP_TRY(randn(&m->lm_head, (size_t)V * H));
     KVHP_TRY(ones(&m->final_norm, H));
     m->layers.resize(c.num_layers);
+    // the model's own pages: one block [L][2][Hkv][P][16][D], the layout of a
+    // caller-owned pool (engine::PagedKVCache)
     const size_t pool = (size_t)Hkv * m->P * kPage * D;
-    for (Layer& L : m->layers) {
+    KVHP_TRY(alloc_n(*m, pool * 2 * c.num_layers, &m->pool));
+    KVHP_HIP(hipMemsetAsync(m->pool, 0, pool * 2 * c.num_layers * 2, m->stream),
+             "hipMemsetAsync(pool)");
+    for (int l = 0; l < c.num_layers; ++l) {
+        Layer& L = m->layers[l];
         KVHP_TRY(ones(&L.attn_norm, H));
         KVHP_TRY(ones(&L.ffn_norm, H));
         KVHP_TRY(randn(&L.w_qkv, (size_t)NQKV * H));
         KVHP_TRY(randn(&L.w_o, (size_t)H * Hq * D));
         KVHP_TRY(randn(&L.w_gate_up, (size_t)2 * F * H));
         KVHP_TRY(randn(&L.w_down, (size_t)H * F));
-        KVHP_TRY(alloc_n(*m, pool, &L.pool_k));
-        KVHP_TRY(alloc_n(*m, pool, &L.pool_v));
-        KVHP_HIP(hipMemsetAsync(L.pool_k, 0, pool * 2, m->stream), "hipMemsetAsync(pool)");
-        KVHP_HIP(hipMemsetAsync(L.pool_v, 0, pool * 2, m->stream), "hipMemsetAsync(pool)");
+        L.pool_k = m->pool + (size_t)(2 * l) * pool;
+        L.pool_v = m->pool + (size_t)(2 * l + 1) * pool;
     }
     // identity block table: page i holds positions 16i .. 16i+15
     KVHP_TRY(alloc_n(*m, m->P, &m->bt));
@@ -268,8 +374,7 @@ extern "C" int kvhp_llama_prefill(void* model, const int32_t* tokens, int n, flo
     const kvhp_llama_config& c = m.c;
     KVHP_REQUIRE(n < m.max_ctx, KVHP_ERR_INVALID, "llama_prefill: %d tokens leave no room in %d",
                  n, m.max_ctx);
-    const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
-    const int F = c.ffn_size, NQKV = (Hq + 2 * Hkv) * D;
+    const int H = c.hidden_size;
     void* s = m.stream;
     KVHP_HIP(hipMemcpyAsync(m.tokens, tokens, (size_t)n * 4, hipMemcpyHostToDevice, m.stream),
              "hipMemcpyAsync(tokens)");
@@ -277,19 +382,7 @@ extern "C" int kvhp_llama_prefill(void* model, const int32_t* tokens, int n, flo
     const int32_t st[4] = {n, 0, 0, 0};
     KVHP_HIP(hipMemcpyAsync(m.state, st, sizeof st, hipMemcpyHostToDevice, m.stream),
              "hipMemcpyAsync(state)");
-    KVHP_TRY(kvhp_embedding(m.tokens, m.embed, m.hidden, n, H, c.vocab_size, s));
-    for (const Layer& L : m.layers) {
-        KVHP_TRY(kvhp_rmsnorm(m.hidden, L.attn_norm, m.norm, n, H, c.rms_eps, s));
-        KVHP_TRY(linear(m, m.norm, L.w_qkv, m.qkv, n, NQKV, H, false));
-        KVHP_TRY(kvhp_split_qkv_rope(m.qkv, n, Hq, Hkv, D, 0, c.rope_theta, m.q, m.k, m.v, s));
-        KVHP_TRY(kvhp_flash_prefill_paged(m.q, m.k, m.v, m.attn, n, Hq, Hkv, D, 1, L.pool_k,
-                                          L.pool_v, m.bt, m.P, m.P, s));
-        KVHP_TRY(linear(m, m.attn, L.w_o, m.hidden, n, H, Hq * D, true));
-        KVHP_TRY(kvhp_rmsnorm(m.hidden, L.ffn_norm, m.norm, n, H, c.rms_eps, s));
-        KVHP_TRY(linear(m, m.norm, L.w_gate_up, m.gu, n, 2 * F, H, false));
-        KVHP_TRY(kvhp_swiglu_rows(m.gu, m.act, n, F, s));
-        KVHP_TRY(linear(m, m.act, L.w_down, m.hidden, n, H, F, true));
-    }
+    KVHP_TRY(prefill_layers(m, n, own_pages(m), s));
     // last position only: the decode residual stream continues from it
     KVHP_HIP(hipMemcpyAsync(m.x, m.hidden + (size_t)(n - 1) * H, (size_t)H * 2,
                             hipMemcpyDeviceToDevice, m.stream),
@@ -393,6 +486,62 @@ extern "C" int kvhp_llama_generate(void* model, int n_steps, int use_graph, int3
                  "hipMemcpy(log)");
     }
     return KVHP_OK;
+}
+
+extern "C" int kvhp_llama_prefill_paged(void* model, const int32_t* tokens, int n, void* pool,
+                                        int num_pages, const int32_t* block_table, int max_pages,
+                                        float* logits_out, int32_t* next_token, void* stream) {
+    clear_error();
+    KVHP_REQUIRE(model && tokens && n > 0 && pool && block_table && num_pages > 0 &&
+                     max_pages > 0,
+                 KVHP_ERR_INVALID, "llama_prefill_paged: bad arguments");
+    Model& m = *static_cast<Model*>(model);
+    const kvhp_llama_config& c = m.c;
+    KVHP_REQUIRE(n <= m.max_ctx, KVHP_ERR_INVALID,
+                 "llama_prefill_paged: %d tokens exceed the model's %d activation rows", n,
+                 m.max_ctx);
+    KVHP_REQUIRE((int64_t)n <= (int64_t)max_pages * kPage, KVHP_ERR_INVALID,
+                 "llama_prefill_paged: %d tokens exceed %d pages", n, max_pages);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    BlasOn on(m, s);
+    const Pages pg{static_cast<f16*>(pool), num_pages, block_table, max_pages};
+    KVHP_HIP(hipMemcpyAsync(m.tokens, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s),
+             "hipMemcpyAsync(tokens)");
+    KVHP_TRY(prefill_layers(m, n, pg, s));
+    const int H = c.hidden_size;
+    KVHP_TRY(kvhp_rmsnorm_gemv(m.lm_head, m.hidden + (size_t)(n - 1) * H, m.final_norm, c.rms_eps,
+                               nullptr, m.logits, c.vocab_size, H, s));
+    KVHP_TRY(kvhp_argmax_rows(m.logits, 1, c.vocab_size, m.state + 3, s));
+    if (logits_out)
+        KVHP_HIP(hipMemcpyAsync(logits_out, m.logits, (size_t)c.vocab_size * 4,
+                                hipMemcpyDeviceToHost, s),
+                 "hipMemcpyAsync(logits)");
+    int32_t tok = 0;
+    KVHP_HIP(hipMemcpyAsync(&tok, m.state + 3, 4, hipMemcpyDeviceToHost, s),
+             "hipMemcpyAsync(token)");
+    KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(prefill_paged)");
+    if (next_token) *next_token = tok;
+    return KVHP_OK;
+}
+
+extern "C" int kvhp_llama_decode_paged(void* model, const int32_t* tokens, int batch, void* pool,
+                                       int num_pages, const int32_t* block_tables, int max_pages,
+                                       const int32_t* positions, const int32_t* seq_lens,
+                                       int max_seq_len, float* logits, int32_t* next_tokens,
+                                       void* stream) {
+    clear_error();
+    KVHP_REQUIRE(model && tokens && pool && block_tables && positions && seq_lens && logits &&
+                     next_tokens && num_pages > 0 && max_pages > 0 && max_seq_len > 0,
+                 KVHP_ERR_INVALID, "llama_decode_paged: bad arguments");
+    Model& m = *static_cast<Model*>(model);
+    if (batch == 0) return KVHP_OK;
+    KVHP_REQUIRE(batch > 0 && batch <= m.max_ctx, KVHP_ERR_INVALID,
+                 "llama_decode_paged: batch %d outside 1..%d", batch, m.max_ctx);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    BlasOn on(m, s);
+    const Pages pg{static_cast<f16*>(pool), num_pages, block_tables, max_pages};
+    return decode_rows(m, tokens, batch, pg, positions, seq_lens, max_seq_len, logits, next_tokens,
+                       s);
 }
 
 extern "C" int kvhp_llama_tensor(void* model, int layer, int which, void** ptr, size_t* count) {

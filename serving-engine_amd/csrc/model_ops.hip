@@ -401,9 +401,12 @@ __global__ void rope_kernel(f16* q, f16* k, int64_t S, int Hq, int Hkv, int D, i
 }
 
 // Split the fused QKV projection [S][(Hq + 2Hkv) D] into contiguous q, k, v
-// with RoPE applied to q and k.
+// with RoPE applied to q and k.  Row s sits at position start_pos + s, or at
+// positions[s] (device int32; negative = an idle batch row, rotated as 0)
+// when positions is given.
 __global__ void split_qkv_rope_kernel(const f16* qkv, int64_t S, int Hq, int Hkv, int D,
-                                      int start_pos, float theta, f16* q, f16* k, f16* v) {
+                                      int start_pos, const int32_t* positions, float theta,
+                                      f16* q, f16* k, f16* v) {
     const int half = D / 2;
     const int H = Hq + 2 * Hkv;
     const int64_t pairs = S * (int64_t)H * half;
@@ -419,7 +422,8 @@ __global__ void split_qkv_rope_kernel(const f16* qkv, int64_t S, int Hq, int Hkv
         float o1 = x1, o2 = x2;
         if (h < Hq + Hkv) {
             float c, sn;
-            rope_cs(static_cast<int>(start_pos + s), i, D, theta, c, sn);
+            const int pos = positions ? max(positions[s], 0) : static_cast<int>(start_pos + s);
+            rope_cs(pos, i, D, theta, c, sn);
             o1 = x1 * c - x2 * sn;
             o2 = x2 * c + x1 * sn;
             dst = h < Hq ? q + (s * Hq + h) * D : k + (s * Hkv + (h - Hq)) * D;
@@ -468,11 +472,14 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i) {
     return (static_cast<uint64_t>(ord) << 32) | static_cast<uint64_t>(~i);
 }
 
+// Workgroup r reduces row r of logits [gridDim.x][n] into token[r].
 __global__ void __launch_bounds__(1024)
 argmax_kernel(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, int32_t* log,
               int32_t* log_count, const f16* embed, int64_t hidden, f16* x) {
     __shared__ uint64_t red[16];
     __shared__ int32_t tok_lds;
+    logits += blockIdx.x * n;
+    token += blockIdx.x;
     uint64_t best = 0;  // below every candidate (a NaN candidate has ~i > 0)
     // Thread t scans float4 groups t, t + 1024, ... (all of a pass's loads
     // in flight), then the scalar tail.
@@ -723,9 +730,26 @@ extern "C" int kvhp_split_qkv_rope(const void* qkv, int64_t seq_len, int num_q_h
     hipLaunchKernelGGL(split_qkv_rope_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), static_cast<const f16*>(qkv), seq_len,
                        num_q_heads, num_kv_heads, head_dim, static_cast<int>(start_pos),
-                       rope_theta, static_cast<f16*>(q), static_cast<f16*>(k),
-                       static_cast<f16*>(v));
+                       static_cast<const int32_t*>(nullptr), rope_theta, static_cast<f16*>(q),
+                       static_cast<f16*>(k), static_cast<f16*>(v));
     return check_launch("split_qkv_rope");
+}
+
+extern "C" int kvhp_split_qkv_rope_rows(const void* qkv, int64_t rows, int num_q_heads,
+                                        int num_kv_heads, int head_dim, const int32_t* positions,
+                                        float rope_theta, void* q, void* k, void* v,
+                                        void* stream) {
+    clear_error();
+    if (rows <= 0) return KVHP_OK;
+    KVHP_REQUIRE(qkv && positions && q && k && v && head_dim > 0 && head_dim % 2 == 0 &&
+                     num_q_heads > 0 && num_kv_heads > 0,
+                 KVHP_ERR_INVALID, "split_qkv_rope_rows: bad arguments");
+    const int64_t pairs = rows * (num_q_heads + 2 * num_kv_heads) * (head_dim / 2);
+    hipLaunchKernelGGL(split_qkv_rope_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const f16*>(qkv), rows,
+                       num_q_heads, num_kv_heads, head_dim, 0, positions, rope_theta,
+                       static_cast<f16*>(q), static_cast<f16*>(k), static_cast<f16*>(v));
+    return check_launch("split_qkv_rope_rows");
 }
 
 extern "C" int kvhp_swiglu(const void* gate, const void* up, void* out, int64_t count,
@@ -774,6 +798,20 @@ extern "C" int kvhp_argmax(const float* logits, int64_t n, int32_t* token, int32
     hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
                        logits, n, token, seq_len, log, log_count, nullptr, int64_t{0}, nullptr);
     return check_launch("argmax");
+}
+
+extern "C" int kvhp_argmax_rows(const float* logits, int64_t rows, int64_t n, int32_t* tokens,
+                                void* stream) {
+    clear_error();
+    if (rows <= 0) return KVHP_OK;
+    KVHP_REQUIRE(logits && tokens && n > 0 && n < (int64_t)1 << 31 && rows <= 0x7fffffff,
+                 KVHP_ERR_INVALID, "argmax_rows: bad arguments");
+    hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(rows)), dim3(1024), 0,
+                       static_cast<hipStream_t>(stream), logits, n, tokens,
+                       static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr),
+                       static_cast<int32_t*>(nullptr), static_cast<const f16*>(nullptr),
+                       int64_t{0}, static_cast<f16*>(nullptr));
+    return check_launch("argmax_rows");
 }
 
 namespace kvhp {

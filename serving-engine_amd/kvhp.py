@@ -90,10 +90,13 @@ _SIGNATURES = {
     "kvhp_rmsnorm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
     "kvhp_apply_rope": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp]),
     "kvhp_split_qkv_rope": (_i32, [_vp, _i64, _i32, _i32, _i32, _i64, _f32, _vp, _vp, _vp, _vp]),
+    "kvhp_split_qkv_rope_rows": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _f32, _vp, _vp, _vp,
+                                        _vp]),
     "kvhp_swiglu": (_i32, [_vp, _vp, _vp, _i64, _vp]),
     "kvhp_swiglu_rows": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "kvhp_embedding": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "kvhp_argmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "kvhp_argmax_rows": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "kvhp_randn_f16": (_i32, [_vp, _i64, _u64, _u64, _f32, _vp]),
     "kvhp_fill_f16": (_i32, [_vp, _i64, _f32, _vp]),
     # model runner
@@ -104,6 +107,9 @@ _SIGNATURES = {
     "kvhp_llama_generate": (_i32, [_vp, _i32, _i32, _vp, _vp]),
     "kvhp_llama_tensor": (_i32, [_vp, _i32, _i32, ctypes.POINTER(ctypes.c_void_p),
                                  ctypes.POINTER(ctypes.c_size_t)]),
+    "kvhp_llama_prefill_paged": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "kvhp_llama_decode_paged": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _i32,
+                                       _vp, _vp, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -311,6 +317,13 @@ def split_qkv_rope(qkv, seq_len, num_q_heads, num_kv_heads, head_dim, start_pos,
                                       _stream(stream)))
 
 
+def split_qkv_rope_rows(qkv, rows, num_q_heads, num_kv_heads, head_dim, positions, theta, q, k,
+                        v, stream=None):
+    _check(load().kvhp_split_qkv_rope_rows(_ptr(qkv), rows, num_q_heads, num_kv_heads, head_dim,
+                                           _ptr(positions), theta, _ptr(q), _ptr(k), _ptr(v),
+                                           _stream(stream)))
+
+
 def swiglu(gate, up, out, count, stream=None):
     _check(load().kvhp_swiglu(_ptr(gate), _ptr(up), _ptr(out), count, _stream(stream)))
 
@@ -327,6 +340,10 @@ def embedding(token_ids, table, out, n, hidden, vocab, stream=None):
 def argmax(logits, n, token, seq_len=None, log=None, log_count=None, stream=None):
     _check(load().kvhp_argmax(_ptr(logits), n, _ptr(token), _ptr(seq_len), _ptr(log),
                               _ptr(log_count), _stream(stream)))
+
+
+def argmax_rows(logits, rows, n, tokens, stream=None):
+    _check(load().kvhp_argmax_rows(_ptr(logits), rows, n, _ptr(tokens), _stream(stream)))
 
 
 def randn_f16(out, seed, stream_id, std, stream=None):
@@ -408,6 +425,30 @@ class LlamaModel:
         _check(load().kvhp_llama_generate(self._h, n_steps, int(use_graph), out.ctypes.data,
                                           ctypes.byref(ms)))
         return out, float(ms.value)
+
+    def prefill_paged(self, tokens, pool, num_pages: int, block_table, max_pages: int,
+                      stream=None):
+        """Runner.prefill over a caller-owned pool [L][2][Hkv][num_pages][16][D]
+        (torch fp16) and one block-table row (torch int32, device): returns
+        (first greedy token, fp32 logits of the last position)."""
+        np = self._np
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.config.vocab_size, np.float32)
+        nxt = ctypes.c_int32()
+        _check(load().kvhp_llama_prefill_paged(self._h, t.ctypes.data, t.size, _ptr(pool),
+                                               num_pages, _ptr(block_table), max_pages,
+                                               logits.ctypes.data, ctypes.byref(nxt),
+                                               _stream(stream)))
+        return int(nxt.value), logits
+
+    def decode_paged(self, tokens, pool, num_pages: int, block_tables, max_pages: int, positions,
+                     seq_lens, max_seq_len: int, logits, next_tokens, stream=None):
+        """Runner.decode_step for tokens.numel() sequences; every argument is a
+        device tensor (int32, fp16 pool, fp32 logits [B][V]); asynchronous."""
+        _check(load().kvhp_llama_decode_paged(self._h, _ptr(tokens), tokens.numel(), _ptr(pool),
+                                              num_pages, _ptr(block_tables), max_pages,
+                                              _ptr(positions), _ptr(seq_lens), max_seq_len,
+                                              _ptr(logits), _ptr(next_tokens), _stream(stream)))
 
     def tensor(self, layer: int, which: int):
         """Host copy (numpy float16) of a model tensor."""

@@ -27,6 +27,7 @@
 #include "kv_cache.h"
 #include "kv_view.h"
 #include "kvhp_oracle.h"
+#include "llama_runner.h"
 
 using namespace engine;
 
@@ -674,6 +675,88 @@ void case_paged_prefix_sharing() {
     EXPECT(bad_share, "prefix longer than the source accepted");
 }
 
+void case_llama_runner_paged() {
+    // LlamaRunner over a PagedKVCache (Runner.prefill / decode_step,
+    // docs/runner_interface.md:18-53): three sequences, the third sharing the
+    // first's two full prompt pages, then batched decode steps with an idle
+    // fourth slot.  Each slot against a batch-1 model of the same seed fed the
+    // same tokens: prefill logits bit-identical; decode logits within 2% of
+    // the logit scale, a differing greedy token only at a near-tie (top-1 /
+    // top-2 margin of the batch-1 logits below 0.05).
+    const kvhp_llama_config c = {1024, 256, 2, 4, 2, 64, 512, 1e-5f, 10000.f, 0};
+    const uint64_t seed = 31;
+    const int V = c.vocab_size;
+    LlamaRunner runner(c, seed, 64);
+    PagedKVCache cache(c.num_layers, c.num_kv_heads, c.head_dim, 32, 4, 8);
+    std::mt19937 rng(77);
+    std::uniform_int_distribution<int> tokd(0, V - 1);
+    std::vector<std::vector<int32_t>> prompts(3);
+    prompts[0].resize(35);
+    prompts[1].resize(19);
+    for (int s = 0; s < 2; ++s)
+        for (auto& t : prompts[s]) t = tokd(rng);
+    prompts[2].assign(prompts[0].begin(), prompts[0].begin() + 32);
+    for (int i = 0; i < 7; ++i) prompts[2].push_back(tokd(rng));
+    void* ref[3] = {};
+    for (auto& r : ref) KVHP_CHECK(kvhp_llama_create(&c, seed, 64, &r));
+    auto compare = [&](const float* got, const std::vector<float>& want, int tok, int want_tok,
+                       const char* what) {
+        float scale = 1.f, diff = 0.f, top1 = -INFINITY, top2 = -INFINITY;
+        for (int i = 0; i < V; ++i) {
+            scale = std::max(scale, std::fabs(want[i]));
+            diff = std::max(diff, std::fabs(got[i] - want[i]));
+            if (want[i] > top1) {
+                top2 = top1;
+                top1 = want[i];
+            } else if (want[i] > top2) {
+                top2 = want[i];
+            }
+        }
+        EXPECT(diff < 0.02f * scale, "%s: max |logit diff| %.4f, scale %.2f", what, diff, scale);
+        EXPECT(tok == want_tok || top1 - top2 < 0.05f, "%s: token %d != %d, margin %.4f", what, tok,
+               want_tok, top1 - top2);
+    };
+    std::vector<int32_t> last(4, 0);
+    for (int s = 0; s < 3; ++s) {
+        EXPECT(cache.add_sequence() == s, "slot %d", s);
+        if (s == 2) EXPECT(cache.share_prefix(2, 0, 35) == 32, "shared prefix");
+        cache.set_seq_len(s, (int)prompts[s].size());
+        std::vector<float> lg, rl(V);
+        const int tok = runner.prefill(cache, s, prompts[s], &lg);
+        int32_t rt = -1;
+        KVHP_CHECK(kvhp_llama_prefill(ref[s], prompts[s].data(), (int)prompts[s].size(), rl.data(), &rt));
+        EXPECT(tok == rt && std::memcmp(lg.data(), rl.data(), (size_t)V * 4) == 0,
+               "slot %d: prefill differs from the batch-1 model (token %d vs %d)", s, tok, rt);
+        last[s] = tok;
+    }
+    EXPECT(cache.page_refs(cache.host_block_table(0)[0]) == 2, "shared page refs");
+    bool threw = false;
+    try {
+        runner.prefill(cache, 1, prompts[0]);   // length 19 != 35
+    } catch (const std::logic_error&) {
+        threw = true;
+    }
+    EXPECT(threw, "prefill with a length other than the slot's accepted");
+    for (int st = 0; st < 4; ++st) {
+        std::vector<float> lg;
+        const std::vector<int32_t> next = runner.decode_step(cache, 4, last, &lg);
+        EXPECT(next[3] == -1, "inactive slot got token %d", next[3]);
+        for (int s = 0; s < 3; ++s) {
+            std::vector<float> rl(V);
+            int32_t rt = -1;
+            KVHP_CHECK(kvhp_llama_decode_step(ref[s], last[s], rl.data(), &rt));
+            char what[64];
+            std::snprintf(what, sizeof what, "step %d slot %d", st, s);
+            compare(lg.data() + (size_t)s * V, rl, next[s], rt, what);
+            EXPECT(cache.seq_len(s) == (int)prompts[s].size() + st + 1, "%s: length", what);
+        }
+        for (int s = 0; s < 3; ++s) last[s] = next[s];
+    }
+    for (auto r : ref) kvhp_llama_destroy(r);
+    for (int s = 0; s < 3; ++s) cache.release(s);
+    EXPECT(cache.free_page_count() == cache.num_pages(), "pages leaked");
+}
+
 struct Case {
     const char* name;
     bool gpu;
@@ -702,6 +785,7 @@ int main(int argc, char** argv) {
         {"paged_serving_steps", true, case_paged_serving_steps},
         {"paged_cache_rejects", true, case_paged_cache_rejects},
         {"paged_prefix_sharing", true, case_paged_prefix_sharing},
+        {"llama_runner_paged", true, case_llama_runner_paged},
     };
     for (const Case& c : cases) {
         if (c.gpu && !gpu) continue;

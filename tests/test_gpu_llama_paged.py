@@ -1,0 +1,182 @@
+"""Batched serving over caller-owned pages (kvhp_llama_prefill_paged /
+kvhp_llama_decode_paged): the reference runner contract
+(docs/runner_interface.md:18-53) with the page pool and block tables in the
+caller's hands.
+
+Several sequences live in one pool whose pages are dealt out in a seeded
+random order.  One of them shares another's first two full pages ("share"
+prefix mode: its prefill writes go through a table in which the shared
+pages are -1).  Each is checked against a batch-1 model with the same seed
+(same weights) fed the same tokens:
+  * prefill logits are bit-identical (the same kernels run on the same
+    prompt; only the page placement and the skipped shared-page writes
+    differ);
+  * batched decode logits agree to 2% of the logit scale (B-row GEMMs
+    against the batch-1 GEMVs: fp16 activations rounded in another order),
+    and every greedy token that differs sits at a near-tie (top-1/top-2
+    margin of the batch-1 logits < 0.05);
+  * one sequence's decode logits also against the CPU restatement of the
+    reference forward (oracle/llama_oracle.py), same bound;
+  * the shared pages keep the first sequence's K/V bit for bit through the
+    second's prefill and every decode step, and pages no table names stay
+    zero (an idle batch row, position -1 and no pages, writes nothing).
+    Whether the skipped writes would have changed any bit is left to the
+    C++ engine test, which recomputes the shared prefix with other K/V.
+"""
+import numpy as np
+import pytest
+
+import kvhp
+from llama_oracle import LlamaOracle, top2_margin
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+NEAR_TIE = 0.05
+PAGE = 16
+
+
+def _cfg():
+    return kvhp.LlamaConfig(2048, 512, 3, 8, 2, 64, 1024, 1e-5, 10000.0, 0)
+
+
+def _weights(model, cfg):
+    f32 = lambda a: a.astype(np.float32)
+    v, h, f = cfg.vocab_size, cfg.hidden_size, cfg.ffn_size
+    nqkv = (cfg.num_q_heads + 2 * cfg.num_kv_heads) * cfg.head_dim
+    w = {"embed": f32(model.tensor(-1, kvhp.LLAMA_EMBED)).reshape(v, h),
+         "lm_head": f32(model.tensor(-1, kvhp.LLAMA_LM_HEAD)).reshape(v, h),
+         "final_norm": f32(model.tensor(-1, kvhp.LLAMA_FINAL_NORM)), "layers": []}
+    for li in range(cfg.num_layers):
+        w["layers"].append({
+            "attn_norm": f32(model.tensor(li, kvhp.LLAMA_ATTN_NORM)),
+            "ffn_norm": f32(model.tensor(li, kvhp.LLAMA_FFN_NORM)),
+            "w_qkv": f32(model.tensor(li, kvhp.LLAMA_W_QKV)).reshape(nqkv, h),
+            "w_o": f32(model.tensor(li, kvhp.LLAMA_W_O)).reshape(h, h),
+            "w_gate_up": f32(model.tensor(li, kvhp.LLAMA_W_GATE_UP)).reshape(2 * f, h),
+            "w_down": f32(model.tensor(li, kvhp.LLAMA_W_DOWN)).reshape(h, f)})
+    return w
+
+
+def _close(got, ref, what):
+    scale = max(float(np.abs(ref).max()), 1.0)
+    diff = float(np.abs(got - ref).max())
+    assert diff < 0.02 * scale, f"{what}: max |logit diff| {diff:.4f} (scale {scale:.2f})"
+    tok, rtok = int(np.argmax(got)), int(np.argmax(ref))
+    if tok != rtok:
+        assert top2_margin(ref) < NEAR_TIE, f"{what}: token {tok} != {rtok} outside a near-tie"
+    return diff
+
+
+def test_paged_runner_matches_batch1_runner_and_oracle():
+    cfg = _cfg()
+    L, Hkv, D, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
+    seed, max_ctx, steps = 21, 128, 5
+    P, max_pages = 48, 8
+    rng = np.random.default_rng(4242)
+    dev = "cuda"
+
+    model = kvhp.LlamaModel(cfg, seed=seed, max_ctx=max_ctx)
+    pool = torch.zeros(L * 2 * Hkv * P * PAGE * D, dtype=torch.float16, device=dev)
+
+    # sequences 0-2 own their pages; sequence 3 shares sequence 0's first
+    # two (full) pages and continues with its own suffix
+    lens = [37, 21, 50]
+    prompts = [rng.integers(0, V, n).astype(np.int32) for n in lens]
+    prompts.append(np.concatenate([prompts[0][:32], rng.integers(0, V, 9).astype(np.int32)]))
+    order = rng.permutation(P).tolist()
+    tables = np.full((5, max_pages), -1, np.int32)      # row 4: an idle batch row
+    refs = np.zeros(P, np.int32)
+
+    def take(n):
+        out = [order.pop() for _ in range(n)]
+        refs[out] += 1
+        return out
+
+    for s in range(3):
+        tables[s, :(lens[s] + steps + PAGE - 1) // PAGE] = take((lens[s] + steps + PAGE - 1) // PAGE)
+    tables[3, :2] = tables[0, :2]
+    refs[tables[0, :2]] += 1
+    n3 = (len(prompts[3]) + steps + PAGE - 1) // PAGE
+    tables[3, 2:n3] = take(n3 - 2)
+    write_tables = np.where((tables >= 0) & (refs[np.maximum(tables, 0)] > 1), -1, tables)
+    bt = torch.from_numpy(tables).to(dev)
+    wbt = torch.from_numpy(write_tables).to(dev)
+    assert write_tables[3, 0] == -1 and write_tables[0, 0] == -1 and write_tables[3, 2] >= 0
+
+    # references: one batch-1 model per sequence, same seed = same weights
+    singles = [kvhp.LlamaModel(cfg, seed=seed, max_ctx=max_ctx) for _ in range(4)]
+    first, prefill_logits = [], []
+    pool5 = pool.view(L, 2, Hkv, P, PAGE, D)
+    for s in range(4):
+        # sequence 0 writes its shared pages itself (it owns them first): its
+        # prefill goes through the block table, the others through the write
+        # table.  Prefill attends the recomputed prompt, so even sequence 3
+        # matches its batch-1 model bit for bit.
+        row = bt[0] if s == 0 else wbt[s]
+        tok, lg = model.prefill_paged(prompts[s], pool, P, row, max_pages)
+        rtok, rlg = singles[s].prefill(prompts[s])
+        assert np.array_equal(lg, rlg), f"sequence {s}: prefill logits differ"
+        assert tok == rtok
+        first.append(tok)
+        prefill_logits.append(lg)
+        if s == 0:   # sequence 0's prompt K/V on the pages sequence 3 will share
+            torch.cuda.synchronize()
+            k0 = [pool5[:, :, :, int(tables[0, i])].clone() for i in range(2)]
+
+    oracle = LlamaOracle(cfg, _weights(model, cfg), nthreads=8)
+    _close(prefill_logits[1], oracle.forward(prompts[1]), "sequence 1 prefill vs oracle")
+
+    B = 5
+    cur = list(first) + [0]
+    seq = [len(p) for p in prompts] + [0]
+    logits = torch.empty(B, V, dtype=torch.float32, device=dev)
+    nxt = torch.empty(B, dtype=torch.int32, device=dev)
+    diffs = []
+    for st in range(steps):
+        # bump, then write at num_tokens - 1; the idle row gets position -1, 0 keys
+        pos = np.array([seq[b] if b < 4 else -1 for b in range(B)], np.int32)
+        sl = np.array([seq[b] + 1 if b < 4 else 0 for b in range(B)], np.int32)
+        model.decode_paged(torch.tensor(cur, dtype=torch.int32, device=dev), pool, P, bt,
+                           max_pages, torch.from_numpy(pos).to(dev), torch.from_numpy(sl).to(dev),
+                           int(sl.max()), logits, nxt)
+        torch.cuda.synchronize()
+        got = logits.cpu().numpy()
+        toks = nxt.cpu().numpy()
+        for b in range(4):
+            assert toks[b] == int(np.argmax(got[b])), "device argmax != host argmax of its logits"
+            _, rlg = singles[b].decode_step(int(cur[b]))   # teacher-forced, same token
+            diffs.append(_close(got[b], rlg, f"step {st} sequence {b}"))
+        olg = oracle.forward([int(cur[1])])
+        diffs.append(_close(got[1], olg, f"step {st} sequence 1 vs oracle"))
+        cur = [int(t) for t in toks[:4]] + [0]
+        seq = [x + 1 for x in seq[:4]] + [0]
+    print(f"max |logit diff| batched vs batch-1 / oracle: {max(diffs):.4f}")
+
+    # shared pages unchanged by sequence 3's prefill and every decode step;
+    # pages in no table never written
+    for i in range(2):
+        assert torch.equal(pool5[:, :, :, int(tables[0, i])], k0[i])
+    unused = sorted(set(range(P)) - set(tables[tables >= 0].tolist()))
+    assert unused and all(bool((pool5[:, :, :, p] == 0).all()) for p in unused)
+    for m in singles:
+        m.close()
+    model.close()
+
+
+def test_paged_runner_argument_errors():
+    cfg = _cfg()
+    model = kvhp.LlamaModel(cfg, seed=3, max_ctx=32)
+    pool = torch.zeros(cfg.num_layers * 2 * cfg.num_kv_heads * 4 * PAGE * cfg.head_dim,
+                       dtype=torch.float16, device="cuda")
+    bt = torch.arange(4, dtype=torch.int32, device="cuda")
+    with pytest.raises(kvhp.KVHPError):
+        model.prefill_paged(np.zeros(33, np.int32), pool, 4, bt, 4)    # > max_ctx rows
+    with pytest.raises(kvhp.KVHPError):
+        model.prefill_paged(np.zeros(20, np.int32), pool, 4, bt, 1)    # > 16 * max_pages
+    t = torch.zeros(33, dtype=torch.int32, device="cuda")
+    out = torch.empty(33, cfg.vocab_size, dtype=torch.float32, device="cuda")
+    with pytest.raises(kvhp.KVHPError):                                 # batch > max_ctx
+        model.decode_paged(t, pool, 4, bt, 4, t, t, 16, out, t)
+    model.close()

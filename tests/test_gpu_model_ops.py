@@ -166,6 +166,29 @@ def test_rope_and_split_qkv(s, hq, hkv, d, start):
     assert np.array_equal(_cpu(v2), v.astype(np.float32))
 
 
+def test_split_qkv_rope_rows_per_row_positions():
+    """Batched decode: row r rotated at positions[r] (negative = idle row,
+    rotated as position 0); each row against the oracle's RoPE of that one
+    row at that position."""
+    hq, hkv, d = 8, 2, 64
+    pos = np.array([0, 5, 2047, -1, 16, 4095, 1], np.int32)
+    rows = pos.size
+    rng = np.random.default_rng(77)
+    qkv = oracle.normal_f16(rng, (rows, hq + 2 * hkv, d))
+    q2 = torch.empty((rows, hq, d), dtype=torch.float16, device="cuda")
+    k2 = torch.empty((rows, hkv, d), dtype=torch.float16, device="cuda")
+    v2 = torch.empty((rows, hkv, d), dtype=torch.float16, device="cuda")
+    kvhp.split_qkv_rope_rows(to_gpu(qkv), rows, hq, hkv, d, to_gpu(pos), 10000.0, q2, k2, v2)
+    torch.cuda.synchronize()
+    for r in range(rows):
+        q = np.ascontiguousarray(qkv[r:r + 1, :hq])
+        k = np.ascontiguousarray(qkv[r:r + 1, hq:hq + hkv])
+        rq, rk = oracle.apply_rope(q, k, hq, hkv, d, max(int(pos[r]), 0), 10000.0)
+        _close(_cpu(q2[r]).reshape(-1), _f16(rq).reshape(-1), f"row {r} q")
+        _close(_cpu(k2[r]).reshape(-1), _f16(rk).reshape(-1), f"row {r} k")
+    assert np.array_equal(_cpu(v2), qkv[:, hq + hkv:].astype(np.float32))
+
+
 @pytest.mark.parametrize("rows,n", [(1, 5632), (2048, 5632), (3, 7)])
 def test_swiglu(rows, n):
     rng = np.random.default_rng(rows * n)
@@ -221,6 +244,23 @@ def test_argmax_ties_nan_and_counters():
     assert int(seq.item()) == 10 + len(cases)
     assert int(cnt.item()) == len(cases)
     assert log.cpu().numpy()[:len(cases)].tolist() == [c[1] for c in cases]
+
+
+def test_argmax_rows():
+    """One workgroup per row, the same tie and NaN rules as the single-row
+    argmax; rows of a length that is not a multiple of 4 (unaligned rows)."""
+    rng = np.random.default_rng(10)
+    for n in (32000, 1001):
+        x = rng.standard_normal((6, n)).astype(np.float32)
+        x[1, [40, 9, 700]] = 9.0                 # tie: lowest index wins
+        x[2, :] = -np.inf                        # all -inf -> 0
+        x[3, [0, 1]] = np.nan
+        x[3, n - 1] = 12.0                       # NaN never wins
+        want = [int(np.argmax(x[0])), 9, 0, n - 1, int(np.argmax(x[4])), int(np.argmax(x[5]))]
+        tok = torch.full((6,), -1, dtype=torch.int32, device="cuda")
+        kvhp.argmax_rows(torch.from_numpy(x).cuda(), 6, n, tok)
+        torch.cuda.synchronize()
+        assert tok.cpu().numpy().tolist() == want, n
 
 
 def test_randn_and_fill():
