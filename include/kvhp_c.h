@@ -221,6 +221,28 @@ int kvhp_rmsnorm_qkv_rope_append(const void* W_qkv, const void* x, const void* n
                                  void* pool_k, void* pool_v, const int32_t* block_table,
                                  int max_pages, int num_pages, int num_q_heads, int num_kv_heads,
                                  int head_dim, int K, void* stream);
+/* Batched decode projections: the four fused GEMVs above for `batch`
+ * sequences at once (1 <= batch <= 32), x / outputs row-major [batch][...].
+ * Each weight element is read once per call for all rows (a skinny GEMM on
+ * v_mfma_f32_16x16x32_f16); epilogues and roundings as the batch-1 calls.
+ * K must be 256*n (n <= 8), or 352*n (n <= 16) for kvhp_gemv_residual_rows;
+ * head_dim a multiple of 32 for the QKV call; otherwise
+ * KVHP_ERR_UNSUPPORTED.  The QKV call rotates row b at positions[b]
+ * (device int32) and writes its k / v into page
+ * block_tables[b][positions[b] / 16] (rows [batch][max_pages]); a negative
+ * position marks an idle row (q written, nothing appended). */
+int kvhp_gemv_residual_rows(const void* W, const void* x, const void* r, void* y, int N, int K,
+                            int batch, void* stream);
+int kvhp_rmsnorm_gemv_rows(const void* W, const void* x, const void* norm_w, float eps, void* y16,
+                           float* y32, int N, int K, int batch, void* stream);
+int kvhp_rmsnorm_gemv_swiglu_rows(const void* W_gate_up, const void* x, const void* norm_w,
+                                  float eps, void* out, int N, int K, int batch, void* stream);
+int kvhp_rmsnorm_qkv_rope_append_rows(const void* W_qkv, const void* x, const void* norm_w,
+                                      float eps, const int32_t* positions, float rope_theta,
+                                      void* q_out, void* pool_k, void* pool_v,
+                                      const int32_t* block_tables, int max_pages, int num_pages,
+                                      int num_q_heads, int num_kv_heads, int head_dim, int K,
+                                      int batch, void* stream);
 /* Replaces engine::cuda::rmsnorm (kernels.h:24-32): rows x dim, fp32 math. */
 int kvhp_rmsnorm(const void* x, const void* weight, void* out, int64_t rows, int64_t dim,
                  float eps, void* stream);
@@ -345,8 +367,9 @@ int kvhp_llama_prefill_paged(void* model, const int32_t* tokens, int n, void* po
  * [max_pages] (-1: an idle row, nothing written), attends over seq_lens[b]
  * keys (<= max_seq_len; the caller has already bumped it, so positions[b] =
  * seq_lens[b] - 1), and ends in fp32 logits [batch][V] and greedy
- * next_tokens[batch] (lowest index on ties).  Each projection is one
- * batch-row GEMM.  Asynchronous on `stream`. */
+ * next_tokens[batch] (lowest index on ties).  Up to 32 sequences run on the
+ * fused batched projections (kvhp_*_rows: each weight read once per step);
+ * larger batches on library GEMMs.  Asynchronous on `stream`. */
 int kvhp_llama_decode_paged(void* model, const int32_t* tokens, int batch, void* pool,
                             int num_pages, const int32_t* block_tables, int max_pages,
                             const int32_t* positions, const int32_t* seq_lens, int max_seq_len,

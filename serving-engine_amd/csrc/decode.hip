@@ -793,24 +793,10 @@ bool view_fast_ok(const kvhp_kv_view& v) {
 }
 
 
-// Split-kernel workgroups (one wave each) resident on the device at once:
-// compute units x workgroups per CU, queried once per kernel instance.
+// Split-kernel workgroups (one wave each) resident on the device at once.
 template <typename K>
 int resident_splits(K kernel) {
-    static const int per_cu = [kernel] {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kWave, 0) != hipSuccess)
-            n = 0;
-        return n;
-    }();
-    static const int cus = [] {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            n = 0;
-        return n;
-    }();
-    return per_cu * cus;
+    return resident_workgroups(reinterpret_cast<const void*>(kernel), kWave);
 }
 
 template <int D, int G>

@@ -11,7 +11,9 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "kvhp_c.h"
 
@@ -55,6 +57,31 @@ int argmax_embed(const float* logits, int64_t n, int32_t* token, int32_t* seq_le
 
 inline bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Workgroups of `kernel` (blocks of `threads`) resident on the current
+// device at once: CUs x the occupancy limit, queried once per kernel and
+// block size; 0 if the runtime cannot tell.
+inline int resident_workgroups(const void* kernel, int threads) {
+    struct Entry {
+        const void* kernel;
+        int threads, n;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+        if (e.kernel == kernel && e.threads == threads) return e.n;
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+        hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+        (void)hipGetLastError();
+        per_cu = 0;
+    }
+    const int n = per_cu > 0 && cus > 0 ? per_cu * cus : 0;
+    cache.push_back(Entry{kernel, threads, n});
+    return n;
 }
 
 // -------------------------------------------------------------- device ----

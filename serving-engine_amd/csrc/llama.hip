@@ -81,6 +81,7 @@ struct Model {
     void* ws = nullptr;        // decode attention workspace
     size_t ws_bytes = 0;
     int prompt_len = 0;
+    bool rows_ok = false;      // batched projections fit the skinny-GEMM kernels
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
 
@@ -210,7 +211,9 @@ int prefill_layers(Model& m, int n, const Pages& pg, void* s) {
 
 // One batched decode step: row b takes token tokens[b] at position
 // positions[b] (its K/V appended there through row b of pg.bt) and attends
-// over seq_lens[b] keys; fp32 logits [B][V], greedy tokens next[b].
+// over seq_lens[b] keys; fp32 logits [B][V], greedy tokens next[b].  Up to 32
+// rows run on the fused skinny-GEMM kernels; larger batches on library GEMMs
+// with separate RMSNorm / RoPE / SwiGLU launches.
 int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                 const int32_t* positions, const int32_t* seq_lens, int max_seq_len,
                 float* logits, int32_t* next, void* s) {
@@ -218,6 +221,27 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
     const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
     const int F = c.ffn_size, NQKV = (Hq + 2 * Hkv) * D;
     KVHP_TRY(kvhp_embedding(tokens, m.embed, m.hidden, B, H, c.vocab_size, s));
+    if (B <= 32 && m.rows_ok) {
+        // Skinny-GEMM projections with the batch-1 step's fusions: every
+        // weight read once per step for all B rows, six launches per layer.
+        for (int l = 0; l < c.num_layers; ++l) {
+            const Layer& L = m.layers[l];
+            KVHP_TRY(kvhp_rmsnorm_qkv_rope_append_rows(
+                L.w_qkv, m.hidden, L.attn_norm, c.rms_eps, positions, c.rope_theta, m.q,
+                layer_pool(m, pg, l, 0), layer_pool(m, pg, l, 1), pg.bt, pg.max_pages,
+                pg.num_pages, Hq, Hkv, D, H, B, s));
+            const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
+            KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, seq_lens, m.attn, B, Hq, Hkv, D,
+                                           max_seq_len, 0, nullptr, 0, s));
+            KVHP_TRY(kvhp_gemv_residual_rows(L.w_o, m.attn, m.hidden, m.hidden, H, Hq * D, B, s));
+            KVHP_TRY(kvhp_rmsnorm_gemv_swiglu_rows(L.w_gate_up, m.hidden, L.ffn_norm, c.rms_eps,
+                                                   m.act, F, H, B, s));
+            KVHP_TRY(kvhp_gemv_residual_rows(L.w_down, m.act, m.hidden, m.hidden, H, F, B, s));
+        }
+        KVHP_TRY(kvhp_rmsnorm_gemv_rows(m.lm_head, m.hidden, m.final_norm, c.rms_eps, nullptr,
+                                        logits, c.vocab_size, H, B, s));
+        return kvhp_argmax_rows(logits, B, c.vocab_size, next, s);
+    }
     for (int l = 0; l < c.num_layers; ++l) {
         const Layer& L = m.layers[l];
         KVHP_TRY(kvhp_rmsnorm(m.hidden, L.attn_norm, m.norm, B, H, c.rms_eps, s));
@@ -353,6 +377,10 @@ extern "C" int kvhp_llama_create(const kvhp_llama_config* cfg, uint64_t seed, in
     KVHP_TRY(alloc_n(*m, S, &m->tokens));
     KVHP_TRY(alloc_n(*m, 4, &m->state));
     KVHP_TRY(alloc_n(*m, S, &m->log));
+    // K = hidden (q/k/v, gate/up, LM head), Hq*D (o) and ffn (down): 256*n
+    // with n <= 8, or 352*n with n <= 16 for the down projection
+    auto k256 = [](int K) { return K % 256 == 0 && K / 256 <= 8; };
+    m->rows_ok = k256(H) && (k256(F) || (F % 352 == 0 && F / 352 <= 16)) && D % 32 == 0;
     m->ws_bytes = kvhp_decode_workspace_bytes(1, Hq, Hkv, D, max_ctx, 0);
     KVHP_TRY(alloc(*m, m->ws_bytes, &m->ws));
     KVHP_HIP(hipStreamSynchronize(m->stream), "hipStreamSynchronize(create)");

@@ -28,12 +28,15 @@
 // so that a captured decode step needs no host round trip.
 #include "kvhp_internal.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace kvhp {
 
 namespace {
 
+
+constexpr int kNumCUs = 256;  // MI355X compute units (tile-size heuristic only)
 
 enum Epilogue : int { kEpiF16 = 0, kEpiResidual = 1, kEpiF32 = 2, kEpiSwiglu = 3, kEpiQKV = 4 };
 
@@ -356,6 +359,362 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
         hipLaunchKernelGGL((gemv_generic_kernel<EPI, RMS>), dim3(units), dim3(kWave), 0, s, a);
     }
     return check_launch("gemv");
+}
+
+// ---- Batched decode projections (B <= 32 sequences per step) -----------------
+// Y[b][n] = sum_k W[n][k] X[b][k] on v_mfma_f32_16x16x32_f16 with the weights
+// as the A operand.  A tile is 16 weight rows; for the paired epilogues its
+// first 8 rows pair with its last 8 (SwiGLU: gate rows n..n+7 with up rows
+// N+n..N+n+7; RoPE: dims d..d+7 with d+D/2..d+D/2+7 of one head).  The NW
+// waves of a workgroup split K into slices of 32*C (wave w: k in
+// [32Cw, 32C(w+1))) and keep their slice of X (all B rows: NBT tiles of 16,
+// zero past B; RMSNorm applied once) in registers, while the workgroup walks
+// tiles blockIdx.x, +gridDim.x, ... (grid = the resident workgroups): the
+// next tile's weights are loaded before the current tile's MFMAs, and the
+// epilogue's own reads (residual) before those, so each wave keeps a tile of
+// loads in flight while it computes and reduces.  Lane (g, col) = (l/16,
+// l%16) loads row col of a tile at k = 32t + 8g (16 bytes; an instruction
+// reads 64 contiguous bytes of 16 rows) and the same k of batch row col; the
+// accumulator holds D[4g + e][col].  The NW partial tiles meet in LDS (two
+// buffers, one barrier per tile) and are summed in wave order
+// (deterministic), then the batch-1 GEMV's epilogue runs per (row, batch
+// row).  RMSNorm: the waves' sums of squares of their slices meet in LDS
+// first, so the operand is fp16(x * rs * w) as the batch-1 kernel rounds it.
+struct RowsArgs {
+    const f16* W;          // [rows][K]
+    const f16* x;          // [B][K]
+    const f16* norm_w;     // [K] RMSNorm weight, or null
+    float eps;
+    int N, K, B;
+    int tiles;             // weight tiles
+    int live;              // distinct weight rows per tile: 16, or 8 when tiles are
+                           // scarce (lanes past it repeat rows; their outputs are dropped)
+    f16* y16;              // [B][ldy] (QKV: q [B][Hq*D])
+    float* y32;            // [B][ldy]
+    const f16* resid;      // [B][ldy], may alias y16
+    int ldy;
+    int Hq, Hkv, D;
+    const int32_t* positions;  // [B] write position of each row (QKV); < 0: idle row
+    float theta;
+    f16* pool_k;           // [Hkv][num_pages][16][D]
+    f16* pool_v;
+    const int32_t* bt;     // [B][max_pages]
+    int max_pages, num_pages;
+};
+
+template <int C, int NWMAX, int NBT, int EPI, bool RMS>
+__global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs a) {
+    constexpr bool kPair = EPI == kEpiSwiglu || EPI == kEpiQKV;
+    constexpr int kOut = 256;                 // (row, column) slots per batch tile and weight tile
+    const int L = a.live, P = a.live / 2;     // live rows; row pairs (paired epilogues)
+    // Past ~128 VGPRs (16 waves per workgroup) x is not kept: each tile loads
+    // its batch tiles in turn into one set of registers, and the weights are
+    // not double-buffered.
+    constexpr bool kSeq = !RMS && NBT > 1 && (1 + NBT) * C * 4 > 120;
+    // Two weight buffers where the registers allow (8-wave workgroups);
+    // otherwise each tile loads its weights at its start.
+    constexpr bool kDB = !kSeq && (NWMAX <= 8 || (2 + NBT) * C * 4 <= 100);
+    __shared__ float red[2][NWMAX][NBT][256];
+    __shared__ float ssq[NBT][NWMAX][16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int NW = static_cast<int>(blockDim.x >> 6);
+    const int g = lane >> 4, col = lane & 15;
+    const int ks = w * 32 * C + 8 * g;
+    const int G = static_cast<int>(gridDim.x);
+    const int n_my = (a.tiles - static_cast<int>(blockIdx.x) + G - 1) / G;
+
+    auto load_w = [&](int tile, half8 (&wr)[C]) {
+        int row;
+        const int j = col % L;   // live row of this lane
+        if constexpr (EPI == kEpiQKV) {
+            const int tph = a.D / L;
+            const int hh = tile / tph, d0 = P * (tile % tph);
+            row = hh * a.D + (j < P ? 0 : a.D / 2) + d0 + (j % P);
+        } else if constexpr (EPI == kEpiSwiglu) {
+            const int n = min(P * tile + (j % P), a.N - 1);
+            row = j < P ? n : a.N + n;
+        } else {
+            row = min(L * tile + j, a.N - 1);
+        }
+        const f16* wp = a.W + (int64_t)row * a.K + ks;
+#pragma unroll
+        for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(wp + 32 * t);
+    };
+    auto load_x = [&](int bt, half8 (&xs)[C]) {
+        const int b = min(16 * bt + col, a.B - 1);
+#pragma unroll
+        for (int t = 0; t < C; ++t) xs[t] = load_half8(a.x + (int64_t)b * a.K + ks + 32 * t);
+    };
+
+    half8 wa[C], wb[C];
+    int tile = static_cast<int>(blockIdx.x);
+    if constexpr (kDB) load_w(tile, wa);
+
+    // x slice of every batch tile, resident for all tiles (RMSNorm applied)
+    half8 xr[kSeq ? 1 : NBT][C];
+    if constexpr (!kSeq) {
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) load_x(bt, xr[bt]);
+        half8 nw[C];
+        if constexpr (RMS) {
+#pragma unroll
+            for (int t = 0; t < C; ++t) nw[t] = load_half8(a.norm_w + ks + 32 * t);
+        }
+        // every load above in flight before the first use (one round trip;
+        // the scheduler would otherwise pair loads with their uses)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+            if (16 * bt + col >= a.B)
+#pragma unroll
+                for (int t = 0; t < C; ++t) xr[bt][t] = half8{};
+        if constexpr (RMS) {
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) {
+                float ss = 0.f;
+#pragma unroll
+                for (int t = 0; t < C; ++t)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float v = static_cast<float>(xr[bt][t][e]);
+                        ss = fmaf(v, v, ss);
+                    }
+                ss = rows4_sum(ss);
+                if (g == 0) ssq[bt][w][col] = ss;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) {
+                float tot = 0.f;
+                for (int i = 0; i < NW; ++i) tot += ssq[bt][i][col];
+                const float rs = 1.f / sqrtf(tot / static_cast<float>(a.K) + a.eps);
+#pragma unroll
+                for (int t = 0; t < C; ++t)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        xr[bt][t][e] = static_cast<f16>(static_cast<float>(xr[bt][t][e]) * rs *
+                                                        static_cast<float>(nw[t][e]));
+            }
+        }
+    }
+
+    // This thread's first output of a tile: batch row b0 (the same for every
+    // tile); for the QKV epilogue its write position and page, loaded once.
+    const int o0 = static_cast<int>(threadIdx.x);
+    const int b0 = 16 * (o0 / kOut) + (o0 & 15);
+    int pos0 = -1, pid0 = -1;
+    if constexpr (EPI == kEpiQKV) {
+        if (o0 < NBT * kOut && b0 < a.B) {
+            pos0 = a.positions[b0];
+            if (pos0 >= 0 && (pos0 >> 4) < a.max_pages)
+                pid0 = a.bt[(int64_t)b0 * a.max_pages + (pos0 >> 4)];
+        }
+    }
+
+    // Output o of a tile from its reduced sums; rv: the residual of that
+    // output (Residual epilogue).
+    auto epilogue = [&](int tl, int o, int rb, float rv, int pos, int pid) {
+        const int bt = o / kOut, rem = o % kOut, m = rem >> 4, n = rem & 15;
+        const int b = 16 * bt + n;
+        if (b >= a.B || m >= (kPair ? P : L)) return;
+        float v0 = 0.f, v1 = 0.f;
+        for (int i = 0; i < NW; ++i) {
+            v0 += red[rb][i][bt][m * 16 + n];
+            if constexpr (kPair) v1 += red[rb][i][bt][(m + P) * 16 + n];
+        }
+        if constexpr (EPI == kEpiQKV) {
+            const int tph = a.D / L;
+            const int hh = tl / tph, d = P * (tl % tph) + m, half = a.D / 2;
+            const float x1 = round16(v0), x2 = round16(v1);
+            float o1 = x1, o2 = x2;
+            if (hh < a.Hq + a.Hkv) {
+                float c, sn;
+                rope_cs(pos < 0 ? 0 : pos, d, a.D, a.theta, c, sn);
+                o1 = x1 * c - x2 * sn;
+                o2 = x2 * c + x1 * sn;
+            }
+            if (hh < a.Hq) {
+                f16* q = a.y16 + (int64_t)b * a.ldy + hh * a.D;
+                q[d] = static_cast<f16>(o1);
+                q[d + half] = static_cast<f16>(o2);
+                return;
+            }
+            if (pid < 0 || pid >= a.num_pages) return;
+            const bool isk = hh < a.Hq + a.Hkv;
+            const int kvh = isk ? hh - a.Hq : hh - a.Hq - a.Hkv;
+            f16* dst = (isk ? a.pool_k : a.pool_v) +
+                       (((int64_t)kvh * a.num_pages + pid) * kPage + (pos & 15)) * a.D;
+            dst[d] = static_cast<f16>(o1);
+            dst[d + half] = static_cast<f16>(o2);
+        } else if constexpr (EPI == kEpiSwiglu) {
+            const int nn = P * tl + m;
+            if (nn < a.N)
+                a.y16[(int64_t)b * a.ldy + nn] = static_cast<f16>(silu_mul(round16(v0), round16(v1)));
+        } else {
+            const int nn = L * tl + m;
+            if (nn >= a.N) return;
+            const int64_t yo = (int64_t)b * a.ldy + nn;
+            if constexpr (EPI == kEpiF32)
+                a.y32[yo] = v0;
+            else if constexpr (EPI == kEpiResidual)
+                a.y16[yo] = static_cast<f16>(v0 + rv);
+            else
+                a.y16[yo] = static_cast<f16>(v0);
+        }
+    };
+
+    // One tile: residual read, next tile's weights (pf), MFMAs, partial sums
+    // to LDS buffer rb, barrier, epilogue.
+    auto step = [&](int tl, half8 (&cur)[C], half8 (&nxt)[C], int rb, bool pf) {
+        f16 r0 = static_cast<f16>(0.f);
+        if constexpr (EPI == kEpiResidual) {
+            const int nn = min(L * tl + min((o0 % kOut) / 16, L - 1), a.N - 1);
+            if (o0 < NBT * kOut && b0 < a.B) r0 = a.resid[(int64_t)b0 * a.ldy + nn];
+        }
+        if (pf && kDB) load_w(tl + G, nxt);
+        if constexpr (!kDB) load_w(tl, cur);
+        __builtin_amdgcn_sched_barrier(0);
+        floatx4 acc[NBT];
+        if constexpr (kSeq) {
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) {
+                half8 xs[C];
+                load_x(bt, xs);
+                __builtin_amdgcn_sched_barrier(0);
+                if (16 * bt + col >= a.B)
+#pragma unroll
+                    for (int t = 0; t < C; ++t) xs[t] = half8{};
+                acc[bt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < C; ++t)
+                    acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur[t], xs[t], acc[bt], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) {
+                acc[bt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < C; ++t)
+                    acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur[t], xr[bt][t], acc[bt], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[rb][w][bt][(4 * g + e) * 16 + col] = acc[bt][e];
+        __syncthreads();
+        for (int o = o0; o < NBT * kOut; o += static_cast<int>(blockDim.x)) {
+            if (o == o0) {
+                epilogue(tl, o, rb, static_cast<float>(r0), pos0, pid0);
+            } else {
+                const int b = 16 * (o / kOut) + (o & 15);
+                float rv = 0.f;
+                int pos = -1, pid = -1;
+                if (b < a.B) {
+                    if constexpr (EPI == kEpiResidual)
+                        rv = static_cast<float>(
+                            a.resid[(int64_t)b * a.ldy +
+                                    min(L * tl + min((o % kOut) / 16, L - 1), a.N - 1)]);
+                    if constexpr (EPI == kEpiQKV) {
+                        pos = a.positions[b];
+                        if (pos >= 0 && (pos >> 4) < a.max_pages)
+                            pid = a.bt[(int64_t)b * a.max_pages + (pos >> 4)];
+                    }
+                }
+                epilogue(tl, o, rb, rv, pos, pid);
+            }
+        }
+    };
+
+    // Tiles in pairs so that the two weight buffers keep fixed registers; the
+    // last tile of the workgroup issues no prefetch.
+    for (int i = 0;;) {
+        if (i + 1 < n_my) {
+            step(tile, wa, wb, 0, true);
+        } else {
+            step(tile, wa, wb, 0, false);
+            break;
+        }
+        tile += G;
+        ++i;
+        if (i + 1 < n_my) {
+            step(tile, wb, wa, 1, true);
+        } else {
+            step(tile, wb, wa, 1, false);
+            break;
+        }
+        tile += G;
+        ++i;
+    }
+}
+
+// Slice shape for K: C = 8 (8 x 16 bytes per lane and row) with K/256 <= 8
+// waves, or C = 11 with K/352 <= 16 waves (K = 5632: 16 waves).  Other K, or
+// B > 32: unsupported (the caller keeps the library GEMM).
+bool rows_shape(int K, int& C, int& NW) {
+    if (K % 256 == 0 && K / 256 >= 1 && K / 256 <= 8) {
+        C = 8;
+        NW = K / 256;
+        return true;
+    }
+    if (K % 352 == 0 && K / 352 >= 1 && K / 352 <= 16) {
+        C = 11;
+        NW = K / 352;
+        return true;
+    }
+    return false;
+}
+
+template <int C, int NWMAX, int NBT, int EPI, bool RMS>
+void launch_rows_k(const RowsArgs& a, int NW, hipStream_t s) {
+    auto kern = gemm_rows_kernel<C, NWMAX, NBT, EPI, RMS>;
+    // one workgroup per resident slot, each walking its share of the tiles
+    const int slots = resident_workgroups(reinterpret_cast<const void*>(kern), kWave * NW);
+    const int grid = slots > 0 ? std::min(a.tiles, slots) : a.tiles;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kWave * NW), 0, s, a);
+}
+
+template <int C, int NWMAX, int EPI, bool RMS>
+void launch_rows_c(const RowsArgs& a, int NW, hipStream_t s) {
+    if (a.B <= 16)
+        launch_rows_k<C, NWMAX, 1, EPI, RMS>(a, NW, s);
+    else
+        launch_rows_k<C, NWMAX, 2, EPI, RMS>(a, NW, s);
+}
+
+template <int EPI, bool RMS>
+int launch_rows(RowsArgs a, hipStream_t s, const char* what) {
+    int C = 0, NW = 0;
+    KVHP_REQUIRE(a.B >= 1 && a.B <= 32, KVHP_ERR_UNSUPPORTED, "%s: batch %d outside 1..32", what,
+                 a.B);
+    KVHP_REQUIRE(rows_shape(a.K, C, NW), KVHP_ERR_UNSUPPORTED,
+                 "%s: K=%d is neither 256*n (n <= 8) nor 352*n (n <= 16)", what, a.K);
+    KVHP_REQUIRE(aligned16(a.W) && aligned16(a.x) && (!RMS || aligned16(a.norm_w)),
+                 KVHP_ERR_UNSUPPORTED, "%s: W, x and the norm weight must be 16-byte aligned",
+                 what);
+    // 16 live rows per tile, or 8 when 16 leaves CUs idle and 8 still fits
+    // one tile per CU (a second round of tiles costs more than idle CUs)
+    auto tiles_for = [&](int live) {
+        if constexpr (EPI == kEpiQKV)
+            return (a.Hq + 2 * a.Hkv) * (a.D / live);
+        else if constexpr (EPI == kEpiSwiglu)
+            return (a.N + live / 2 - 1) / (live / 2);
+        else
+            return (a.N + live - 1) / live;
+    };
+    a.live = tiles_for(16) < kNumCUs && tiles_for(8) <= kNumCUs ? 8 : 16;
+    a.tiles = tiles_for(a.live);
+    if (C == 8) {
+        launch_rows_c<8, 8, EPI, RMS>(a, NW, s);
+    } else {
+        if constexpr (EPI == kEpiResidual && !RMS)
+            launch_rows_c<11, 16, EPI, RMS>(a, NW, s);
+        else
+            return fail(KVHP_ERR_UNSUPPORTED, "%s: K=%d needs the 352-wide slices, which only the "
+                        "residual projection has", what, a.K);
+    }
+    return check_launch(what);
 }
 
 // Row-wise RMSNorm (prefill): one workgroup of 256 threads per row.
@@ -686,6 +1045,115 @@ extern "C" int kvhp_rmsnorm_qkv_rope_append(const void* W_qkv, const void* x, co
     a.max_pages = max_pages;
     a.num_pages = num_pages;
     return launch_gemv<kEpiQKV, true>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvhp_gemv_residual_rows(const void* W, const void* x, const void* r, void* y,
+                                       int N, int K, int batch, void* stream) {
+    clear_error();
+    if (N == 0 || batch == 0) return KVHP_OK;
+    int rc = check_gemv(W, x, N, K, "gemv_residual_rows");
+    if (rc) return rc;
+    KVHP_REQUIRE(r && y, KVHP_ERR_INVALID, "gemv_residual_rows: null residual/output");
+    RowsArgs a{};
+    a.W = static_cast<const f16*>(W);
+    a.x = static_cast<const f16*>(x);
+    a.N = N;
+    a.K = K;
+    a.B = batch;
+    a.resid = static_cast<const f16*>(r);
+    a.y16 = static_cast<f16*>(y);
+    a.ldy = N;
+    return launch_rows<kEpiResidual, false>(a, static_cast<hipStream_t>(stream),
+                                               "gemv_residual_rows");
+}
+
+extern "C" int kvhp_rmsnorm_gemv_rows(const void* W, const void* x, const void* norm_w, float eps,
+                                      void* y16, float* y32, int N, int K, int batch,
+                                      void* stream) {
+    clear_error();
+    if (N == 0 || batch == 0) return KVHP_OK;
+    int rc = check_gemv(W, x, N, K, "rmsnorm_gemv_rows");
+    if (rc) return rc;
+    KVHP_REQUIRE(norm_w, KVHP_ERR_INVALID, "rmsnorm_gemv_rows: null norm weight");
+    KVHP_REQUIRE((y16 != nullptr) != (y32 != nullptr), KVHP_ERR_INVALID,
+                 "rmsnorm_gemv_rows: give exactly one of y16 / y32");
+    RowsArgs a{};
+    a.W = static_cast<const f16*>(W);
+    a.x = static_cast<const f16*>(x);
+    a.norm_w = static_cast<const f16*>(norm_w);
+    a.eps = eps;
+    a.N = N;
+    a.K = K;
+    a.B = batch;
+    a.y16 = static_cast<f16*>(y16);
+    a.y32 = y32;
+    a.ldy = N;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return y32 ? launch_rows<kEpiF32, true>(a, s, "rmsnorm_gemv_rows")
+               : launch_rows<kEpiF16, true>(a, s, "rmsnorm_gemv_rows");
+}
+
+extern "C" int kvhp_rmsnorm_gemv_swiglu_rows(const void* W_gate_up, const void* x,
+                                             const void* norm_w, float eps, void* out, int N,
+                                             int K, int batch, void* stream) {
+    clear_error();
+    if (N == 0 || batch == 0) return KVHP_OK;
+    int rc = check_gemv(W_gate_up, x, N, K, "rmsnorm_gemv_swiglu_rows");
+    if (rc) return rc;
+    KVHP_REQUIRE(norm_w && out, KVHP_ERR_INVALID, "rmsnorm_gemv_swiglu_rows: null pointer");
+    RowsArgs a{};
+    a.W = static_cast<const f16*>(W_gate_up);
+    a.x = static_cast<const f16*>(x);
+    a.norm_w = static_cast<const f16*>(norm_w);
+    a.eps = eps;
+    a.N = N;
+    a.K = K;
+    a.B = batch;
+    a.y16 = static_cast<f16*>(out);
+    a.ldy = N;
+    return launch_rows<kEpiSwiglu, true>(a, static_cast<hipStream_t>(stream),
+                                            "rmsnorm_gemv_swiglu_rows");
+}
+
+extern "C" int kvhp_rmsnorm_qkv_rope_append_rows(
+    const void* W_qkv, const void* x, const void* norm_w, float eps, const int32_t* positions,
+    float rope_theta, void* q_out, void* pool_k, void* pool_v, const int32_t* block_tables,
+    int max_pages, int num_pages, int num_q_heads, int num_kv_heads, int head_dim, int K,
+    int batch, void* stream) {
+    clear_error();
+    if (batch == 0) return KVHP_OK;
+    const int N = (num_q_heads + 2 * num_kv_heads) * head_dim;
+    int rc = check_gemv(W_qkv, x, N, K, "rmsnorm_qkv_rope_append_rows");
+    if (rc) return rc;
+    KVHP_REQUIRE(norm_w && positions && q_out && pool_k && pool_v && block_tables,
+                 KVHP_ERR_INVALID, "rmsnorm_qkv_rope_append_rows: null pointer");
+    KVHP_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 16 == 0,
+                 KVHP_ERR_INVALID,
+                 "rmsnorm_qkv_rope_append_rows: head_dim %d must be a multiple of 16", head_dim);
+    KVHP_REQUIRE(max_pages > 0 && num_pages > 0, KVHP_ERR_INVALID,
+                 "rmsnorm_qkv_rope_append_rows: empty page pool");
+    RowsArgs a{};
+    a.W = static_cast<const f16*>(W_qkv);
+    a.x = static_cast<const f16*>(x);
+    a.norm_w = static_cast<const f16*>(norm_w);
+    a.eps = eps;
+    a.N = N;
+    a.K = K;
+    a.B = batch;
+    a.y16 = static_cast<f16*>(q_out);
+    a.ldy = num_q_heads * head_dim;
+    a.Hq = num_q_heads;
+    a.Hkv = num_kv_heads;
+    a.D = head_dim;
+    a.positions = positions;
+    a.theta = rope_theta;
+    a.pool_k = static_cast<f16*>(pool_k);
+    a.pool_v = static_cast<f16*>(pool_v);
+    a.bt = block_tables;
+    a.max_pages = max_pages;
+    a.num_pages = num_pages;
+    return launch_rows<kEpiQKV, true>(a, static_cast<hipStream_t>(stream),
+                                         "rmsnorm_qkv_rope_append_rows");
 }
 
 extern "C" int kvhp_rmsnorm(const void* x, const void* weight, void* out, int64_t rows,

@@ -87,6 +87,12 @@ _SIGNATURES = {
     "kvhp_rmsnorm_gemv_swiglu": (_i32, [_vp, _vp, _vp, _f32, _vp, _i32, _i32, _vp]),
     "kvhp_rmsnorm_qkv_rope_append": (_i32, [_vp, _vp, _vp, _f32, _vp, _f32, _vp, _vp, _vp, _vp,
                                             _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "kvhp_gemv_residual_rows": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "kvhp_rmsnorm_gemv_rows": (_i32, [_vp, _vp, _vp, _f32, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "kvhp_rmsnorm_gemv_swiglu_rows": (_i32, [_vp, _vp, _vp, _f32, _vp, _i32, _i32, _i32, _vp]),
+    "kvhp_rmsnorm_qkv_rope_append_rows": (_i32, [_vp, _vp, _vp, _f32, _vp, _f32, _vp, _vp, _vp,
+                                                 _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                                 _vp]),
     "kvhp_rmsnorm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
     "kvhp_apply_rope": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp]),
     "kvhp_split_qkv_rope": (_i32, [_vp, _i64, _i32, _i32, _i32, _i64, _f32, _vp, _vp, _vp, _vp]),
@@ -299,6 +305,31 @@ def rmsnorm_qkv_rope_append(W_qkv, x, norm_w, eps, seq_len, theta, q_out, pool_k
         _ptr(W_qkv), _ptr(x), _ptr(norm_w), eps, _ptr(seq_len), theta, _ptr(q_out), _ptr(pool_k),
         _ptr(pool_v), _ptr(block_table), block_table.numel(), pool_k.shape[1], num_q_heads,
         num_kv_heads, head_dim, K, _stream(stream)))
+
+
+def gemv_residual_rows(W, x, r, y, N, K, batch, stream=None):
+    _check(load().kvhp_gemv_residual_rows(_ptr(W), _ptr(x), _ptr(r), _ptr(y), N, K, batch,
+                                          _stream(stream)))
+
+
+def rmsnorm_gemv_rows(W, x, norm_w, eps, N, K, batch, y16=None, y32=None, stream=None):
+    _check(load().kvhp_rmsnorm_gemv_rows(_ptr(W), _ptr(x), _ptr(norm_w), eps, _ptr(y16),
+                                         _ptr(y32), N, K, batch, _stream(stream)))
+
+
+def rmsnorm_gemv_swiglu_rows(W_gate_up, x, norm_w, eps, out, N, K, batch, stream=None):
+    _check(load().kvhp_rmsnorm_gemv_swiglu_rows(_ptr(W_gate_up), _ptr(x), _ptr(norm_w), eps,
+                                                _ptr(out), N, K, batch, _stream(stream)))
+
+
+def rmsnorm_qkv_rope_append_rows(W_qkv, x, norm_w, eps, positions, theta, q_out, pool_k, pool_v,
+                                 block_tables, num_q_heads, num_kv_heads, head_dim, K, batch,
+                                 stream=None):
+    """pool_k / pool_v [Hkv][P][16][D]; block_tables int32 [batch][max_pages]."""
+    _check(load().kvhp_rmsnorm_qkv_rope_append_rows(
+        _ptr(W_qkv), _ptr(x), _ptr(norm_w), eps, _ptr(positions), theta, _ptr(q_out),
+        _ptr(pool_k), _ptr(pool_v), _ptr(block_tables), block_tables.shape[1], pool_k.shape[1],
+        num_q_heads, num_kv_heads, head_dim, K, batch, _stream(stream)))
 
 
 def rmsnorm(x, weight, out, rows, dim, eps, stream=None):

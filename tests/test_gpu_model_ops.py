@@ -132,6 +132,111 @@ def test_rmsnorm_qkv_rope_append(hq, hkv, d, k, pos):
     assert not pk[:, mask].any() and not pv[:, mask].any()
 
 
+# Batched projections: each batch row against the oracle's GEMV of that row
+# (same roundings as the batch-1 kernels), for batch sizes on both sides of
+# the 16-row tile and shapes with a partial last row tile.
+ROWS_BATCHES = [1, 5, 16, 17, 32]
+
+
+@pytest.mark.parametrize("batch", ROWS_BATCHES)
+@pytest.mark.parametrize("n,k", [(2048, 2048), (2048, 5632), (100, 512), (33, 1056)])
+def test_gemv_residual_rows(batch, n, k):
+    rng = np.random.default_rng(batch * 1000 + n + k)
+    W = oracle.normal_f16(rng, (n, k), 0.02)
+    x = oracle.normal_f16(rng, (batch, k))
+    r = oracle.normal_f16(rng, (batch, n))
+    ref = oracle.matmul_transB(x.astype(np.float32), W.astype(np.float32), nthreads=8)
+    y = to_gpu(r)   # in place: y = W x + y
+    kvhp.gemv_residual_rows(to_gpu(W), to_gpu(x), y, y, n, k, batch)
+    torch.cuda.synchronize()
+    _close(_cpu(y), _f16(ref + r.astype(np.float32)), f"gemv_residual_rows B={batch} {n}x{k}")
+
+
+@pytest.mark.parametrize("batch", ROWS_BATCHES)
+@pytest.mark.parametrize("n,k", [(32000, 2048), (2048, 2048), (77, 512)])
+def test_rmsnorm_gemv_rows(batch, n, k):
+    rng = np.random.default_rng(batch * 7 + n + k)
+    W = oracle.normal_f16(rng, (n, k), 0.02)
+    x = oracle.normal_f16(rng, (batch, k), 3.0)
+    w = (1.0 + oracle.normal_f16(rng, (k,), 0.1).astype(np.float32)).astype(np.float16)
+    xn = _f16(oracle.rmsnorm(x, w, 1e-5))
+    ref = oracle.matmul_transB(xn, W.astype(np.float32), nthreads=8)
+    y32 = torch.empty((batch, n), dtype=torch.float32, device="cuda")
+    y16 = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+    kvhp.rmsnorm_gemv_rows(to_gpu(W), to_gpu(x), to_gpu(w), 1e-5, n, k, batch, y32=y32)
+    kvhp.rmsnorm_gemv_rows(to_gpu(W), to_gpu(x), to_gpu(w), 1e-5, n, k, batch, y16=y16)
+    torch.cuda.synchronize()
+    _close(y32.cpu().numpy(), ref, f"rmsnorm_gemv_rows fp32 B={batch}")
+    _close(_cpu(y16), _f16(ref), f"rmsnorm_gemv_rows fp16 B={batch}")
+
+
+@pytest.mark.parametrize("batch", ROWS_BATCHES)
+@pytest.mark.parametrize("n,k", [(5632, 2048), (37, 2048), (100, 768)])
+def test_rmsnorm_gemv_swiglu_rows(batch, n, k):
+    rng = np.random.default_rng(batch * 11 + n * 3 + k)
+    Wgu = oracle.normal_f16(rng, (2 * n, k), 0.02)
+    x = oracle.normal_f16(rng, (batch, k))
+    w = (1.0 + oracle.normal_f16(rng, (k,), 0.1).astype(np.float32)).astype(np.float16)
+    xn = _f16(oracle.rmsnorm(x, w, 1e-5))
+    gu = _f16(oracle.matmul_transB(xn, Wgu.astype(np.float32), nthreads=8))
+    ref = oracle.swiglu(gu[:, :n], gu[:, n:])
+    out = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+    kvhp.rmsnorm_gemv_swiglu_rows(to_gpu(Wgu), to_gpu(x), to_gpu(w), 1e-5, out, n, k, batch)
+    torch.cuda.synchronize()
+    _close(_cpu(out), _f16(ref), f"rmsnorm_gemv_swiglu_rows B={batch} {n}x{k}")
+
+
+@pytest.mark.parametrize("batch", ROWS_BATCHES)
+@pytest.mark.parametrize("hq,hkv,d,k", [(32, 4, 64, 2048), (8, 2, 128, 2048), (4, 4, 32, 256)])
+def test_rmsnorm_qkv_rope_append_rows(batch, hq, hkv, d, k):
+    rng = np.random.default_rng(batch * 13 + hq + d)
+    n = (hq + 2 * hkv) * d
+    W = oracle.normal_f16(rng, (n, k), 0.02)
+    x = oracle.normal_f16(rng, (batch, k))
+    w = (1.0 + oracle.normal_f16(rng, (k,), 0.1).astype(np.float32)).astype(np.float16)
+    theta = 10000.0
+    max_pages = 4
+    P = batch * max_pages + 3
+    tables = rng.permutation(P)[:batch * max_pages].astype(np.int32).reshape(batch, max_pages)
+    pos = rng.integers(0, 16 * max_pages, batch).astype(np.int32)
+    if batch > 1:
+        pos[1] = -1                                  # an idle row appends nothing
+    xn = _f16(oracle.rmsnorm(x, w, 1e-5))
+    qkv = _f16(oracle.matmul_transB(xn, W.astype(np.float32), nthreads=8))
+    pool_k = torch.zeros((hkv, P, 16, d), dtype=torch.float16, device="cuda")
+    pool_v = torch.zeros_like(pool_k)
+    q_out = torch.empty((batch, hq * d), dtype=torch.float16, device="cuda")
+    kvhp.rmsnorm_qkv_rope_append_rows(to_gpu(W), to_gpu(x), to_gpu(w), 1e-5, to_gpu(pos), theta,
+                                      q_out, pool_k, pool_v, to_gpu(tables), hq, hkv, d, k, batch)
+    torch.cuda.synchronize()
+    pk = pool_k.float().cpu().numpy()
+    pv = pool_v.float().cpu().numpy()
+    qo = _cpu(q_out)
+    written = np.zeros(pk.shape[1:3], bool)
+    for b in range(batch):
+        p0 = max(int(pos[b]), 0)
+        q, kk = oracle.apply_rope(qkv[b, :hq * d], qkv[b, hq * d:(hq + hkv) * d], hq, hkv, d, p0,
+                                  theta)
+        _close(qo[b], _f16(q), f"q row {b}")
+        if pos[b] < 0:
+            continue
+        page, slot = tables[b, pos[b] // 16], pos[b] % 16
+        written[page, slot] = True
+        _close(pk[:, page, slot, :].reshape(-1), _f16(kk), f"k page row {b}")
+        _close(pv[:, page, slot, :].reshape(-1), qkv[b, (hq + hkv) * d:], f"v page row {b}")
+    assert not pk[:, ~written].any() and not pv[:, ~written].any()
+
+
+def test_rows_projection_errors():
+    W = torch.zeros((64, 2048), dtype=torch.float16, device="cuda")
+    x = torch.zeros((40, 2048), dtype=torch.float16, device="cuda")
+    y = torch.zeros((40, 64), dtype=torch.float16, device="cuda")
+    with pytest.raises(kvhp.KVHPError):                  # batch above 32
+        kvhp.gemv_residual_rows(W, x, y, y, 64, 2048, 33)
+    with pytest.raises(kvhp.KVHPError):                  # K not 256*n / 352*n
+        kvhp.gemv_residual_rows(W, x, y, y, 64, 1000, 4)
+
+
 @pytest.mark.parametrize("rows,dim", [(1, 2048), (2048, 2048), (7, 100), (3, 5632), (65, 64)])
 def test_rmsnorm_rows(rows, dim):
     rng = np.random.default_rng(rows + dim)
