@@ -311,7 +311,8 @@ def run_config3(torch, kvhp, args):
         "decode_bytes": dbytes,
         "step_bytes": step_bytes,
         "splits": splits if splits else
-                  f"auto (balanced, {kvhp.decode_auto_splits(b, hkv, d, max_len)} slots)",
+                  f"auto (balanced on the device; workspace for up to "
+                  f"{kvhp.decode_auto_splits(b, hkv, d, max_len)} splits per sequence)",
         "sum_L": int(L1.sum()),
         "c": c,
     }

@@ -42,6 +42,15 @@ int check_launch(const char* what);
 int argmax_embed(const float* logits, int64_t n, int32_t* token, int32_t* seq_len, int32_t* log,
                  int32_t* log_count, const void* embed, int64_t hidden, void* x, hipStream_t s);
 
+// kvhp_rmsnorm_qkv_rope_append for one token at position *position (device
+// int32; negative: nothing appended) rather than at seq_len[0] - 1
+// (model_ops.hip; the batched runner's one-sequence step).
+int rmsnorm_qkv_rope_append_at(const void* W_qkv, const void* x, const void* norm_w, float eps,
+                               const int32_t* position, float rope_theta, void* q_out,
+                               void* pool_k, void* pool_v, const int32_t* block_table,
+                               int max_pages, int num_pages, int num_q_heads, int num_kv_heads,
+                               int head_dim, int K, hipStream_t stream);
+
 #define KVHP_REQUIRE(cond, code, ...)          \
     do {                                       \
         if (!(cond)) return ::kvhp::fail(code, __VA_ARGS__); \

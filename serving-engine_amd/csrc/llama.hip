@@ -211,9 +211,10 @@ int prefill_layers(Model& m, int n, const Pages& pg, void* s) {
 
 // One batched decode step: row b takes token tokens[b] at position
 // positions[b] (its K/V appended there through row b of pg.bt) and attends
-// over seq_lens[b] keys; fp32 logits [B][V], greedy tokens next[b].  Up to 32
-// rows run on the fused skinny-GEMM kernels; larger batches on library GEMMs
-// with separate RMSNorm / RoPE / SwiGLU launches.
+// over seq_lens[b] keys; fp32 logits [B][V], greedy tokens next[b].  One row
+// runs on the batch-1 step's GEMV kernels, up to 32 on the fused skinny-GEMM
+// kernels, larger batches on library GEMMs with separate RMSNorm / RoPE /
+// SwiGLU launches.
 int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                 const int32_t* positions, const int32_t* seq_lens, int max_seq_len,
                 float* logits, int32_t* next, void* s) {
@@ -221,6 +222,27 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
     const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
     const int F = c.ffn_size, NQKV = (Hq + 2 * Hkv) * D;
     KVHP_TRY(kvhp_embedding(tokens, m.embed, m.hidden, B, H, c.vocab_size, s));
+    if (B == 1) {
+        // one sequence: the batch-1 step's GEMV kernels (no padded MFMA columns)
+        for (int l = 0; l < c.num_layers; ++l) {
+            const Layer& L = m.layers[l];
+            KVHP_TRY(rmsnorm_qkv_rope_append_at(L.w_qkv, m.hidden, L.attn_norm, c.rms_eps,
+                                                positions, c.rope_theta, m.q,
+                                                layer_pool(m, pg, l, 0), layer_pool(m, pg, l, 1),
+                                                pg.bt, pg.max_pages, pg.num_pages, Hq, Hkv, D, H,
+                                                static_cast<hipStream_t>(s)));
+            const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
+            KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, seq_lens, m.attn, 1, Hq, Hkv, D,
+                                           max_seq_len, 0, nullptr, 0, s));
+            KVHP_TRY(kvhp_gemv_residual(L.w_o, m.attn, m.hidden, m.hidden, H, Hq * D, s));
+            KVHP_TRY(kvhp_rmsnorm_gemv_swiglu(L.w_gate_up, m.hidden, L.ffn_norm, c.rms_eps, m.act,
+                                              F, H, s));
+            KVHP_TRY(kvhp_gemv_residual(L.w_down, m.act, m.hidden, m.hidden, H, F, s));
+        }
+        KVHP_TRY(kvhp_rmsnorm_gemv(m.lm_head, m.hidden, m.final_norm, c.rms_eps, nullptr, logits,
+                                   c.vocab_size, H, s));
+        return kvhp_argmax_rows(logits, 1, c.vocab_size, next, s);
+    }
     if (B <= 32 && m.rows_ok) {
         // Skinny-GEMM projections with the batch-1 step's fusions: every
         // weight read once per step for all B rows, six launches per layer.

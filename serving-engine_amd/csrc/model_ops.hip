@@ -52,7 +52,8 @@ struct GemvArgs {
     const f16* resid;      // residual added in the epilogue (may alias y16)
     // fused QKV: rows [Hq*D q | Hkv*D k | Hkv*D v]
     int Hq, Hkv, D;
-    const int32_t* seq_len;  // device: the token is at position seq_len[0] - 1
+    const int32_t* seq_len;  // device: the token is at position seq_len[0] - len_offset
+    int len_offset;          // 1: seq_len holds the bumped length; 0: it holds the position
     float theta;
     f16* pool_k;           // [Hkv][num_pages][16][D]
     f16* pool_v;
@@ -145,7 +146,7 @@ __global__ void __launch_bounds__(kWave) gemv_kernel(const GemvArgs a) {
     int pos = 0, pid = -1;
     float rc = 1.f, rs = 0.f;  // RoPE rotation of this lane's pair
     if constexpr (EPI == kEpiQKV) {
-        pos = a.seq_len[0] - 1;
+        pos = a.seq_len[0] - a.len_offset;
         if (pos >= 0 && (pos >> 4) < a.max_pages) pid = a.bt[pos >> 4];
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -292,7 +293,7 @@ __global__ void __launch_bounds__(kWave) gemv_generic_kernel(const GemvArgs a) {
         const float x1 = round16(dot_row(hh * a.D + d));
         const float x2 = round16(dot_row(hh * a.D + d + half));
         if (lane != 0) return;
-        const int pos = a.seq_len[0] - 1;
+        const int pos = a.seq_len[0] - a.len_offset;
         float o1 = x1, o2 = x2;
         if (hh < a.Hq + a.Hkv) {
             float c, s;
@@ -1013,13 +1014,13 @@ extern "C" int kvhp_rmsnorm_gemv_swiglu(const void* W_gate_up, const void* x, co
     return launch_gemv<kEpiSwiglu, true>(a, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int kvhp_rmsnorm_qkv_rope_append(const void* W_qkv, const void* x, const void* norm_w,
-                                            float eps, const int32_t* seq_len, float rope_theta,
-                                            void* q_out, void* pool_k, void* pool_v,
-                                            const int32_t* block_table, int max_pages,
-                                            int num_pages, int num_q_heads, int num_kv_heads,
-                                            int head_dim, int K, void* stream) {
-    clear_error();
+namespace {
+// seq_len[0] - len_offset is the token's position.
+int qkv_rope_append_impl(const void* W_qkv, const void* x, const void* norm_w, float eps,
+                         const int32_t* seq_len, int len_offset, float rope_theta, void* q_out,
+                         void* pool_k, void* pool_v, const int32_t* block_table, int max_pages,
+                         int num_pages, int num_q_heads, int num_kv_heads, int head_dim, int K,
+                         void* stream) {
     const int N = (num_q_heads + 2 * num_kv_heads) * head_dim;
     int rc = check_gemv(W_qkv, x, N, K, "rmsnorm_qkv_rope_append");
     if (rc) return rc;
@@ -1038,6 +1039,7 @@ extern "C" int kvhp_rmsnorm_qkv_rope_append(const void* W_qkv, const void* x, co
     a.Hkv = num_kv_heads;
     a.D = head_dim;
     a.seq_len = seq_len;
+    a.len_offset = len_offset;
     a.theta = rope_theta;
     a.pool_k = static_cast<f16*>(pool_k);
     a.pool_v = static_cast<f16*>(pool_v);
@@ -1046,6 +1048,32 @@ extern "C" int kvhp_rmsnorm_qkv_rope_append(const void* W_qkv, const void* x, co
     a.num_pages = num_pages;
     return launch_gemv<kEpiQKV, true>(a, static_cast<hipStream_t>(stream));
 }
+
+}  // namespace
+
+extern "C" int kvhp_rmsnorm_qkv_rope_append(const void* W_qkv, const void* x, const void* norm_w,
+                                            float eps, const int32_t* seq_len, float rope_theta,
+                                            void* q_out, void* pool_k, void* pool_v,
+                                            const int32_t* block_table, int max_pages,
+                                            int num_pages, int num_q_heads, int num_kv_heads,
+                                            int head_dim, int K, void* stream) {
+    clear_error();
+    return qkv_rope_append_impl(W_qkv, x, norm_w, eps, seq_len, 1, rope_theta, q_out, pool_k,
+                                pool_v, block_table, max_pages, num_pages, num_q_heads,
+                                num_kv_heads, head_dim, K, stream);
+}
+
+namespace kvhp {
+int rmsnorm_qkv_rope_append_at(const void* W_qkv, const void* x, const void* norm_w, float eps,
+                               const int32_t* position, float rope_theta, void* q_out,
+                               void* pool_k, void* pool_v, const int32_t* block_table,
+                               int max_pages, int num_pages, int num_q_heads, int num_kv_heads,
+                               int head_dim, int K, hipStream_t stream) {
+    return qkv_rope_append_impl(W_qkv, x, norm_w, eps, position, 0, rope_theta, q_out, pool_k,
+                                pool_v, block_table, max_pages, num_pages, num_q_heads,
+                                num_kv_heads, head_dim, K, stream);
+}
+}  // namespace kvhp
 
 extern "C" int kvhp_gemv_residual_rows(const void* W, const void* x, const void* r, void* y,
                                        int N, int K, int batch, void* stream) {

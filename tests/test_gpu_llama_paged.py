@@ -205,6 +205,38 @@ def test_paged_runner_large_batch_path_matches_fused_path():
     model.close()
 
 
+def test_paged_runner_single_sequence_step_is_the_batch1_step():
+    """A batch of one runs the batch-1 step's kernels: with the same split
+    plan (max_seq_len = the batch-1 model's context) its logits equal the
+    batch-1 model's bit for bit, over a pool and block table of its own."""
+    cfg = _cfg()
+    L, Hkv, D, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
+    max_ctx, P, max_pages = 96, 40, 6
+    rng = np.random.default_rng(5150)
+    prompt = rng.integers(0, V, 45).astype(np.int32)
+    model = kvhp.LlamaModel(cfg, seed=17, max_ctx=max_ctx)
+    single = kvhp.LlamaModel(cfg, seed=17, max_ctx=max_ctx)
+    pool = torch.zeros(L * 2 * Hkv * P * PAGE * D, dtype=torch.float16, device="cuda")
+    bt = torch.from_numpy(rng.permutation(P)[:max_pages].astype(np.int32)).cuda()
+    tok, lg = model.prefill_paged(prompt, pool, P, bt, max_pages)
+    rtok, rlg = single.prefill(prompt)
+    assert tok == rtok and np.array_equal(lg, rlg)
+    logits = torch.empty(1, V, dtype=torch.float32, device="cuda")
+    nxt = torch.empty(1, dtype=torch.int32, device="cuda")
+    seq = len(prompt)
+    for step in range(4):
+        pos = torch.tensor([seq], dtype=torch.int32, device="cuda")
+        model.decode_paged(torch.tensor([tok], dtype=torch.int32, device="cuda"), pool, P,
+                           bt.view(1, -1), max_pages, pos, pos + 1, max_ctx, logits, nxt)
+        rtok, rlg = single.decode_step(tok)
+        torch.cuda.synchronize()
+        assert np.array_equal(logits.cpu().numpy()[0], rlg), f"step {step}: logits differ"
+        assert int(nxt.item()) == rtok
+        tok, seq = rtok, seq + 1
+    single.close()
+    model.close()
+
+
 def test_paged_runner_argument_errors():
     cfg = _cfg()
     model = kvhp.LlamaModel(cfg, seed=3, max_ctx=32)
