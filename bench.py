@@ -58,11 +58,13 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5,kv")
     ap.add_argument("--profile", nargs="?", const="decode", default=None,
-                    choices=("decode", "prefill", "c5"),
+                    choices=("decode", "prefill", "c5", "batched"),
                     help="short run for rocprofv3: a 256 MiB device copy (counter "
                          "calibration) then the config-3 steps (decode), config-4 "
-                         "S=2048 prefill calls (prefill) or --steps config-5 decode "
-                         "steps without the HIP graph (c5); no CPU baseline, no extras")
+                         "S=2048 prefill calls (prefill), --steps config-5 decode "
+                         "steps without the HIP graph (c5) or --steps batched decode "
+                         "steps of the config-5 model at B = 1, 8, 32 (batched); no "
+                         "CPU baseline, no extras")
     return ap.parse_args()
 
 
@@ -512,6 +514,46 @@ def run_config5_eager(torch, kvhp, steps=32, prompt_len=2048):
             "first_tokens": toks[:8].tolist()}
 
 
+def run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=20, ctx=2048):
+    """The config-5 model serving B sequences at once through the batched
+    runner (kvhp_llama_decode_paged: caller-owned page pool, one block-table
+    row per sequence, eager launches): every sequence prefilled with a
+    seeded ctx-id prompt, then `steps` timed decode steps per batch size."""
+    cfg = kvhp.llama_1b_config()
+    L, hkv, d, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
+    bmax = max(batches)
+    per = (ctx + steps + 8 + 15) // 16
+    P = bmax * per
+    model = kvhp.LlamaModel(cfg, seed=5, max_ctx=max(ctx, bmax))
+    pool = torch.zeros(L * 2 * hkv * P * 16 * d, dtype=torch.float16, device="cuda")
+    bt = torch.arange(P, dtype=torch.int32, device="cuda").view(bmax, per)
+    rng = np.random.default_rng(5)
+    first = [model.prefill_paged(rng.integers(0, V, ctx).astype(np.int32), pool, P, bt[b], per)[0]
+             for b in range(bmax)]
+    logits = torch.empty(bmax, V, dtype=torch.float32, device="cuda")
+    nxt = torch.empty(bmax, dtype=torch.int32, device="cuda")
+    out = {}
+    for B in batches:
+        toks = torch.tensor(first[:B], dtype=torch.int32, device="cuda")
+
+        def step(pos):
+            p = torch.full((B,), pos, dtype=torch.int32, device="cuda")
+            model.decode_paged(toks, pool, P, bt[:B], per, p, p + 1, pos + 1, logits[:B], nxt[:B])
+        for w in range(3):
+            step(ctx + w)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            step(ctx + 3 + i)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        out[f"B{B}"] = {"ms_per_step": round(ms, 4), "tok_s": round(B * 1e3 / ms, 1)}
+    model.close()
+    return {"workload": f"config-5 model, batched runner, ctx {ctx}, eager launches", **out}
+
+
 def traffic_from_profile(dbytes):
     """HBM bytes per decode call from the committed rocprofv3 --pmc summary
     (profiles/decode_config3_traffic.json), if present."""
@@ -531,7 +573,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
-                                   "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+                                   "(multi-GPU sharding is a design, not built)"}))
         sys.exit(2)
     import torch
     import kvhp
@@ -555,6 +597,10 @@ def main():
         if args.profile == "c5":
             r5 = run_config5_eager(torch, kvhp, steps=args.steps)
             print(json.dumps({"profile": "c5", "config5": r5}))
+            return
+        if args.profile == "batched":
+            rb = run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=args.steps)
+            print(json.dumps({"profile": "batched", "config5_batched": rb}))
             return
     log("config3 timed steps ...")
     r = run_config3(torch, kvhp, args)
