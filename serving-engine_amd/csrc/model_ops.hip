@@ -438,13 +438,24 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
             row = min(L * tile + j, a.N - 1);
         }
         const f16* wp = a.W + (int64_t)row * a.K + ks;
+        // lanes past the live rows load nothing (their output rows are dropped)
+        if (col < L) {
 #pragma unroll
-        for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(wp + 32 * t);
+            for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(wp + 32 * t);
+        } else {
+#pragma unroll
+            for (int t = 0; t < C; ++t) wr[t] = half8{};
+        }
     };
     auto load_x = [&](int bt, half8 (&xs)[C]) {
-        const int b = min(16 * bt + col, a.B - 1);
+        const int b = 16 * bt + col;   // columns past B: zero, not loaded
+        if (b < a.B) {
 #pragma unroll
-        for (int t = 0; t < C; ++t) xs[t] = load_half8(a.x + (int64_t)b * a.K + ks + 32 * t);
+            for (int t = 0; t < C; ++t) xs[t] = load_half8(a.x + (int64_t)b * a.K + ks + 32 * t);
+        } else {
+#pragma unroll
+            for (int t = 0; t < C; ++t) xs[t] = half8{};
+        }
     };
 
     half8 wa[C], wb[C];
