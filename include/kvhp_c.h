@@ -361,6 +361,19 @@ int kvhp_llama_tensor(void* model, int layer, int which, void** ptr, size_t* cou
 int kvhp_llama_prefill_paged(void* model, const int32_t* tokens, int n, void* pool,
                              int num_pages, const int32_t* block_table, int max_pages,
                              float* logits_out, int32_t* next_token, void* stream);
+/* prefill(seq) in the "full" prefix mode (runner_interface.md:30-33): the
+ * first num_cached of the n prompt positions (0 < num_cached < n) already
+ * have their K/V in the pages of block_table (a cached, possibly shared,
+ * prefix); only positions [num_cached, n) run through the model, each
+ * attending over the keys up to itself read through block_table, their K/V
+ * appended through write_table (NULL: block_table; pass the write table,
+ * shared pages -1, when a forwarded position lies in a shared page, e.g.
+ * the last token of a fully cached prompt).  Outputs and preconditions as
+ * kvhp_llama_prefill_paged. */
+int kvhp_llama_prefill_cached(void* model, const int32_t* tokens, int n, int num_cached,
+                              void* pool, int num_pages, const int32_t* block_table,
+                              const int32_t* write_table, int max_pages, float* logits_out,
+                              int32_t* next_token, void* stream);
 /* decode_step(seqs) (runner_interface.md:37-53) for `batch` sequences
  * (batch <= max_ctx), all arguments device memory: row b embeds tokens[b],
  * appends its K/V at positions[b] through row b of block_tables [batch]

@@ -35,6 +35,7 @@
 
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <vector>
@@ -78,6 +79,8 @@ struct Model {
     int32_t* state = nullptr;  // [0] seq_len, [1] current token, [2] log count,
                                // [3] token of a paged prefill
     int32_t* log = nullptr;    // [max_ctx] generated tokens
+    int32_t* aux = nullptr;    // cached-prefix prefill: replicated block-table rows, lengths
+    size_t aux_words = 0;
     void* ws = nullptr;        // decode attention workspace
     size_t ws_bytes = 0;
     int prompt_len = 0;
@@ -205,6 +208,74 @@ int prefill_layers(Model& m, int n, const Pages& pg, void* s) {
         KVHP_TRY(linear(m, m.norm, L.w_gate_up, m.gu, n, 2 * F, H, false));
         KVHP_TRY(kvhp_swiglu_rows(m.gu, m.act, n, F, s));
         KVHP_TRY(linear(m, m.act, L.w_down, m.hidden, n, H, F, true));
+    }
+    return KVHP_OK;
+}
+
+// Inputs of a cached-prefix prefill's attention, on the device: row r of
+// tables [rows][width] is the sequence's block-table row, lens[r] =
+// first + r + 1 (query row r sits at position first + r), start[0] = first.
+__global__ void suffix_rows_kernel(int32_t* tables, int32_t* lens, int32_t* start,
+                                   const int32_t* row, int rows, int width, int first) {
+    const int64_t total = (int64_t)rows * width;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x)
+        tables[i] = row[i % width];
+    for (int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; r < rows;
+         r += (int64_t)gridDim.x * blockDim.x)
+        lens[r] = first + static_cast<int32_t>(r) + 1;
+    if (blockIdx.x == 0 && threadIdx.x == 0) start[0] = first;
+}
+
+// "Full" prefix mode: only prompt positions [first, n) run through the
+// model (m.tokens holds all n ids).  Their K/V are appended through
+// write_bt (the block-table row, or it with shared pages set to -1), and
+// query row r attends over keys
+// [0, first + r + 1) from the pages -- the cached prefix included -- as one
+// row of a batched decode-attention call.  Final hidden rows in m.hidden.
+int prefill_suffix_layers(Model& m, int first, int n, const Pages& pg, const int32_t* write_bt,
+                          hipStream_t s) {
+    const kvhp_llama_config& c = m.c;
+    const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
+    const int F = c.ffn_size, NQKV = (Hq + 2 * Hkv) * D;
+    const int S = n - first;
+    const size_t words = (size_t)S * pg.max_pages + S + 1;
+    if (m.aux_words < words) {
+        KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(aux)");
+        if (m.aux) {
+            for (auto& p : m.allocs)
+                if (p == m.aux) p = nullptr;
+            (void)hipFree(m.aux);
+            m.aux = nullptr;
+        }
+        KVHP_TRY(alloc_n(m, words, &m.aux));
+        m.aux_words = words;
+    }
+    int32_t* tables = m.aux;
+    int32_t* lens = tables + (size_t)S * pg.max_pages;
+    int32_t* start = lens + S;
+    const int64_t blocks = std::min<int64_t>(((int64_t)S * pg.max_pages + 255) / 256, 1024);
+    hipLaunchKernelGGL(suffix_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,
+                       tables, lens, start, pg.bt, S, pg.max_pages, first);
+    KVHP_TRY(check_launch("suffix_rows"));
+    const Pages rows_pg{pg.base, pg.num_pages, tables, pg.max_pages};
+    KVHP_TRY(kvhp_embedding(m.tokens + first, m.embed, m.hidden, S, H, c.vocab_size, s));
+    for (int l = 0; l < c.num_layers; ++l) {
+        const Layer& L = m.layers[l];
+        KVHP_TRY(kvhp_rmsnorm(m.hidden, L.attn_norm, m.norm, S, H, c.rms_eps, s));
+        KVHP_TRY(linear(m, m.norm, L.w_qkv, m.qkv, S, NQKV, H, false));
+        KVHP_TRY(kvhp_split_qkv_rope(m.qkv, S, Hq, Hkv, D, first, c.rope_theta, m.q, m.k, m.v, s));
+        KVHP_TRY(kvhp_paged_append_kv(m.k, m.v, layer_pool(m, pg, l, 0), layer_pool(m, pg, l, 1),
+                                      write_bt, pg.max_pages, start, 1, S, Hkv, D, pg.num_pages,
+                                      s));
+        const kvhp_kv_view kv = pages_view(m, rows_pg, l, 0), vv = pages_view(m, rows_pg, l, 1);
+        KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, lens, m.attn, S, Hq, Hkv, D, n, 0, nullptr,
+                                       0, s));
+        KVHP_TRY(linear(m, m.attn, L.w_o, m.hidden, S, H, Hq * D, true));
+        KVHP_TRY(kvhp_rmsnorm(m.hidden, L.ffn_norm, m.norm, S, H, c.rms_eps, s));
+        KVHP_TRY(linear(m, m.norm, L.w_gate_up, m.gu, S, 2 * F, H, false));
+        KVHP_TRY(kvhp_swiglu_rows(m.gu, m.act, S, F, s));
+        KVHP_TRY(linear(m, m.act, L.w_down, m.hidden, S, H, F, true));
     }
     return KVHP_OK;
 }
@@ -538,29 +609,38 @@ extern "C" int kvhp_llama_generate(void* model, int n_steps, int use_graph, int3
     return KVHP_OK;
 }
 
-extern "C" int kvhp_llama_prefill_paged(void* model, const int32_t* tokens, int n, void* pool,
-                                        int num_pages, const int32_t* block_table, int max_pages,
-                                        float* logits_out, int32_t* next_token, void* stream) {
-    clear_error();
+namespace {
+// Prefill over caller pages: positions [first, n) of the n prompt ids run
+// through the model (first = 0: the whole prompt by the flash prefill
+// kernel; first > 0: the suffix attends the cached prefix from the pages);
+// logits and greedy token of the last position.
+int prefill_pages(void* model, const int32_t* tokens, int n, int first, void* pool, int num_pages,
+                  const int32_t* block_table, const int32_t* write_table, int max_pages,
+                  float* logits_out, int32_t* next_token, void* stream, const char* what) {
     KVHP_REQUIRE(model && tokens && n > 0 && pool && block_table && num_pages > 0 &&
                      max_pages > 0,
-                 KVHP_ERR_INVALID, "llama_prefill_paged: bad arguments");
+                 KVHP_ERR_INVALID, "%s: bad arguments", what);
+    KVHP_REQUIRE(first >= 0 && first < n, KVHP_ERR_INVALID,
+                 "%s: %d cached tokens of a %d-token prompt", what, first, n);
     Model& m = *static_cast<Model*>(model);
     const kvhp_llama_config& c = m.c;
     KVHP_REQUIRE(n <= m.max_ctx, KVHP_ERR_INVALID,
-                 "llama_prefill_paged: %d tokens exceed the model's %d activation rows", n,
-                 m.max_ctx);
+                 "%s: %d tokens exceed the model's %d activation rows", what, n, m.max_ctx);
     KVHP_REQUIRE((int64_t)n <= (int64_t)max_pages * kPage, KVHP_ERR_INVALID,
-                 "llama_prefill_paged: %d tokens exceed %d pages", n, max_pages);
+                 "%s: %d tokens exceed %d pages", what, n, max_pages);
     hipStream_t s = static_cast<hipStream_t>(stream);
     BlasOn on(m, s);
     const Pages pg{static_cast<f16*>(pool), num_pages, block_table, max_pages};
     KVHP_HIP(hipMemcpyAsync(m.tokens, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s),
              "hipMemcpyAsync(tokens)");
-    KVHP_TRY(prefill_layers(m, n, pg, s));
+    if (first == 0)
+        KVHP_TRY(prefill_layers(m, n, pg, s));
+    else
+        KVHP_TRY(prefill_suffix_layers(m, first, n, pg, write_table ? write_table : block_table,
+                                       s));
     const int H = c.hidden_size;
-    KVHP_TRY(kvhp_rmsnorm_gemv(m.lm_head, m.hidden + (size_t)(n - 1) * H, m.final_norm, c.rms_eps,
-                               nullptr, m.logits, c.vocab_size, H, s));
+    KVHP_TRY(kvhp_rmsnorm_gemv(m.lm_head, m.hidden + (size_t)(n - first - 1) * H, m.final_norm,
+                               c.rms_eps, nullptr, m.logits, c.vocab_size, H, s));
     KVHP_TRY(kvhp_argmax_rows(m.logits, 1, c.vocab_size, m.state + 3, s));
     if (logits_out)
         KVHP_HIP(hipMemcpyAsync(logits_out, m.logits, (size_t)c.vocab_size * 4,
@@ -569,9 +649,31 @@ extern "C" int kvhp_llama_prefill_paged(void* model, const int32_t* tokens, int 
     int32_t tok = 0;
     KVHP_HIP(hipMemcpyAsync(&tok, m.state + 3, 4, hipMemcpyDeviceToHost, s),
              "hipMemcpyAsync(token)");
-    KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(prefill_paged)");
+    KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(prefill)");
     if (next_token) *next_token = tok;
     return KVHP_OK;
+}
+}  // namespace
+
+extern "C" int kvhp_llama_prefill_paged(void* model, const int32_t* tokens, int n, void* pool,
+                                        int num_pages, const int32_t* block_table, int max_pages,
+                                        float* logits_out, int32_t* next_token, void* stream) {
+    clear_error();
+    return prefill_pages(model, tokens, n, 0, pool, num_pages, block_table, nullptr, max_pages,
+                         logits_out, next_token, stream, "llama_prefill_paged");
+}
+
+extern "C" int kvhp_llama_prefill_cached(void* model, const int32_t* tokens, int n,
+                                         int num_cached, void* pool, int num_pages,
+                                         const int32_t* block_table,
+                                         const int32_t* write_table, int max_pages,
+                                         float* logits_out, int32_t* next_token, void* stream) {
+    clear_error();
+    KVHP_REQUIRE(num_cached > 0, KVHP_ERR_INVALID,
+                 "llama_prefill_cached: no cached tokens (kvhp_llama_prefill_paged runs the "
+                 "whole prompt)");
+    return prefill_pages(model, tokens, n, num_cached, pool, num_pages, block_table, write_table,
+                         max_pages, logits_out, next_token, stream, "llama_prefill_cached");
 }
 
 extern "C" int kvhp_llama_decode_paged(void* model, const int32_t* tokens, int batch, void* pool,

@@ -6,18 +6,22 @@
 // weights (kvhp_llama_create), served over a PagedKVCache whose layer count,
 // KV heads and head dim match the model:
 //
-//   * prefill(cache, slot, prompt): the scheduler has already set the slot's
-//     length to the prompt length (pages reserved; the runner allocates
-//     nothing and leaves the length alone).  K/V of every prompt position go
+//   * prefill(cache, slot, prompt, ..., num_cached): the scheduler has
+//     already set the slot's length to the prompt length (pages reserved;
+//     the runner allocates nothing and leaves the length alone).  K/V go
 //     through the cache's write table, so pages the slot shares with another
-//     sequence keep their cached K/V ("share" prefix mode, :30-33).  Returns
-//     the greedy first token.
+//     sequence keep their cached K/V.  num_cached = 0 recomputes the whole
+//     prompt ("share" prefix mode, :30-33); num_cached > 0 (the tokens
+//     share_prefix() returned) forwards only the rest, which attends to the
+//     cached prefix from the pages ("full" mode).  Returns the greedy first
+//     token.
 //   * decode_step(cache, batch, tokens): "bump, then write at num_tokens - 1"
 //     for every active slot in [0, batch) (PagedKVCache::begin_decode_step,
 //     which throws if a write would land on a shared page, :51), then one
-//     batched step: each projection one batch-row GEMM, attention per slot
-//     over its own block table.  Returns the greedy next token per slot
-//     (-1 for inactive slots).
+//     batched step (up to 32 slots on the batched projections: each weight
+//     read once for all of them), attention per slot over its own block
+//     table.  Returns the greedy next token per slot (-1 for inactive
+//     slots).
 //
 // Calls on one runner must not overlap (they share activation buffers).
 #pragma once
@@ -49,20 +53,34 @@ public:
     LlamaRunner& operator=(const LlamaRunner&) = delete;
 
     int prefill(PagedKVCache& cache, int slot, const std::vector<int32_t>& prompt,
-                std::vector<float>* logits = nullptr, Stream stream = nullptr) {
+                std::vector<float>* logits = nullptr, Stream stream = nullptr,
+                int num_cached = 0) {
         check_cache(cache);
         if (slot < 0 || slot >= cache.max_batch())
             throw std::out_of_range("LlamaRunner::prefill: slot " + std::to_string(slot));
         if (prompt.empty() || cache.seq_len(slot) != (int)prompt.size())
             throw std::logic_error("LlamaRunner::prefill: the slot's length must already be the "
                                    "prompt length (" + std::to_string(prompt.size()) + ")");
+        if (num_cached < 0 || num_cached > (int)prompt.size())
+            throw std::invalid_argument("LlamaRunner::prefill: num_cached " +
+                                        std::to_string(num_cached));
         cache.sync(stream);
         if (logits) logits->resize(config_.vocab_size);
         int32_t tok = -1;
-        KVHP_CHECK(kvhp_llama_prefill_paged(
-            model_, prompt.data(), (int)prompt.size(), cache.raw_data(), cache.num_pages(),
-            cache.write_block_tables() + (size_t)slot * cache.max_pages_per_seq(),
-            cache.max_pages_per_seq(), logits ? logits->data() : nullptr, &tok, stream));
+        const size_t row = (size_t)slot * cache.max_pages_per_seq();
+        if (num_cached > 0) {
+            // a fully cached prompt still forwards its last token
+            const int first = std::min(num_cached, (int)prompt.size() - 1);
+            KVHP_CHECK(kvhp_llama_prefill_cached(
+                model_, prompt.data(), (int)prompt.size(), first, cache.raw_data(),
+                cache.num_pages(), cache.block_tables() + row, cache.write_block_tables() + row,
+                cache.max_pages_per_seq(), logits ? logits->data() : nullptr, &tok, stream));
+        } else {
+            KVHP_CHECK(kvhp_llama_prefill_paged(
+                model_, prompt.data(), (int)prompt.size(), cache.raw_data(), cache.num_pages(),
+                cache.write_block_tables() + row, cache.max_pages_per_seq(),
+                logits ? logits->data() : nullptr, &tok, stream));
+        }
         return tok;
     }
 

@@ -114,6 +114,8 @@ _SIGNATURES = {
     "kvhp_llama_tensor": (_i32, [_vp, _i32, _i32, ctypes.POINTER(ctypes.c_void_p),
                                  ctypes.POINTER(ctypes.c_size_t)]),
     "kvhp_llama_prefill_paged": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "kvhp_llama_prefill_cached": (_i32, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp,
+                                         _vp, _vp]),
     "kvhp_llama_decode_paged": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _i32,
                                        _vp, _vp, _vp]),
 }
@@ -470,6 +472,21 @@ class LlamaModel:
                                                num_pages, _ptr(block_table), max_pages,
                                                logits.ctypes.data, ctypes.byref(nxt),
                                                _stream(stream)))
+        return int(nxt.value), logits
+
+    def prefill_cached(self, tokens, num_cached: int, pool, num_pages: int, block_table,
+                       max_pages: int, write_table=None, stream=None):
+        """Runner.prefill in the "full" prefix mode: the first num_cached
+        positions' K/V are already in the pages; only the rest is forwarded
+        (appends through write_table if given)."""
+        np = self._np
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.config.vocab_size, np.float32)
+        nxt = ctypes.c_int32()
+        _check(load().kvhp_llama_prefill_cached(self._h, t.ctypes.data, t.size, num_cached,
+                                                _ptr(pool), num_pages, _ptr(block_table),
+                                                _ptr(write_table), max_pages, logits.ctypes.data,
+                                                ctypes.byref(nxt), _stream(stream)))
         return int(nxt.value), logits
 
     def decode_paged(self, tokens, pool, num_pages: int, block_tables, max_pages: int, positions,

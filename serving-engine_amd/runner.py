@@ -13,12 +13,15 @@ document:
 * ``BlockTable`` / ``Sequence``: ``physical_block_ids``, ``num_tokens``,
   ``num_cached_tokens``, ``last_token_id``, ``generated_ids``,
   ``last_logits``, ``last_logit_margin``.
-* ``Runner.prefill(seq, allocator=None)`` (:20-35): the prompt runs through
-  the model; its K/V go into ``physical_block_ids[skip_blocks:]`` with
-  ``skip_blocks = num_cached_tokens // block_size`` -- the blocks before
-  are shared and keep their cached K/V ("share" prefix mode: the prompt is
-  recomputed, shared blocks are not overwritten).  Never allocates, never
-  changes ``num_tokens``.  Returns the greedy first token.
+* ``Runner.prefill(seq, allocator=None)`` (:20-35): K/V go into
+  ``physical_block_ids[skip_blocks:]`` with ``skip_blocks =
+  num_cached_tokens // block_size``; the blocks before are shared and keep
+  their cached K/V.  ``prefix_mode="share"`` recomputes the whole prompt
+  (flash prefill) and skips the shared blocks' writes; ``"full"`` forwards
+  only the uncached suffix, which attends to the cached prefix from the
+  pages (when the whole prompt is cached, its last token is forwarded, its
+  write into the shared block dropped).  Never allocates, never changes
+  ``num_tokens``.  Returns the greedy first token.
 * ``Runner.decode_step(seqs, allocator=None)`` (:37-55): bumps every
   sequence's ``num_tokens`` by one, writes its new K/V at
   ``num_tokens - 1``, asserts that the block written is not shared
@@ -129,8 +132,12 @@ def _margin(logits: np.ndarray) -> float:
 class Runner:
     """Runner.prefill / decode_step / step over a page pool this object owns."""
 
-    def __init__(self, model: "kvhp.LlamaModel", num_blocks: int, device: str = "cuda"):
+    def __init__(self, model: "kvhp.LlamaModel", num_blocks: int, device: str = "cuda",
+                 prefix_mode: str = "share"):
         import torch
+        if prefix_mode not in ("share", "full"):
+            raise ValueError(f"prefix_mode must be 'share' or 'full', not {prefix_mode!r}")
+        self.prefix_mode = prefix_mode
         self._torch = torch
         c = model.config
         self.model = model
@@ -166,11 +173,19 @@ class Runner:
         skip = seq.num_cached_tokens // BLOCK_SIZE
         ids = seq.block_table.physical_block_ids
         table = np.array(ids, np.int32)
-        table[:skip] = -1                       # shared blocks: not overwritten
+        write = table.copy()
+        write[:skip] = -1                       # shared blocks: not overwritten
+        prompt = np.asarray(seq.prompt_ids, np.int32)
         with torch.inference_mode():
-            row = torch.from_numpy(table).to(self.device)
-            tok, logits = self.model.prefill_paged(np.asarray(seq.prompt_ids, np.int32),
-                                                   self.pool, self.num_blocks, row, len(ids))
+            wrow = torch.from_numpy(write).to(self.device)
+            if self.prefix_mode == "full" and skip > 0:
+                first = min(skip * BLOCK_SIZE, n - 1)
+                tok, logits = self.model.prefill_cached(
+                    prompt, first, self.pool, self.num_blocks,
+                    torch.from_numpy(table).to(self.device), len(ids), write_table=wrow)
+            else:
+                tok, logits = self.model.prefill_paged(prompt, self.pool, self.num_blocks, wrow,
+                                                       len(ids))
         seq.last_logits = torch.from_numpy(logits)
         seq.last_logit_margin = _margin(logits)
         return tok

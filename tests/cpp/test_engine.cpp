@@ -678,11 +678,13 @@ void case_paged_prefix_sharing() {
 void case_llama_runner_paged() {
     // LlamaRunner over a PagedKVCache (Runner.prefill / decode_step,
     // docs/runner_interface.md:18-53): three sequences, the third sharing the
-    // first's two full prompt pages, then batched decode steps with an idle
-    // fourth slot.  Each slot against a batch-1 model of the same seed fed the
-    // same tokens: prefill logits bit-identical; decode logits within 2% of
-    // the logit scale, a differing greedy token only at a near-tie (top-1 /
-    // top-2 margin of the batch-1 logits below 0.05).
+    // first's two full prompt pages and forwarding only its suffix ("full"
+    // prefix mode), then batched decode steps with an idle fourth slot.  Each
+    // slot against a batch-1 model of the same seed fed the same tokens:
+    // prefill logits bit-identical (within 2% for the cached-prefix one);
+    // decode logits within 2% of the logit scale, a differing greedy token
+    // only at a near-tie (top-1 / top-2 margin of the batch-1 logits below
+    // 0.05).
     const kvhp_llama_config c = {1024, 256, 2, 4, 2, 64, 512, 1e-5f, 10000.f, 0};
     const uint64_t seed = 31;
     const int V = c.vocab_size;
@@ -719,15 +721,21 @@ void case_llama_runner_paged() {
     std::vector<int32_t> last(4, 0);
     for (int s = 0; s < 3; ++s) {
         EXPECT(cache.add_sequence() == s, "slot %d", s);
-        if (s == 2) EXPECT(cache.share_prefix(2, 0, 35) == 32, "shared prefix");
+        int cached = 0;
+        if (s == 2) EXPECT((cached = cache.share_prefix(2, 0, 35)) == 32, "shared prefix");
         cache.set_seq_len(s, (int)prompts[s].size());
         std::vector<float> lg, rl(V);
-        const int tok = runner.prefill(cache, s, prompts[s], &lg);
+        // slot 2 forwards only its uncached suffix ("full" prefix mode)
+        const int tok = runner.prefill(cache, s, prompts[s], &lg, nullptr, cached);
         int32_t rt = -1;
         KVHP_CHECK(kvhp_llama_prefill(ref[s], prompts[s].data(), (int)prompts[s].size(), rl.data(), &rt));
-        EXPECT(tok == rt && std::memcmp(lg.data(), rl.data(), (size_t)V * 4) == 0,
-               "slot %d: prefill differs from the batch-1 model (token %d vs %d)", s, tok, rt);
-        last[s] = tok;
+        if (cached == 0) {
+            EXPECT(tok == rt && std::memcmp(lg.data(), rl.data(), (size_t)V * 4) == 0,
+                   "slot %d: prefill differs from the batch-1 model (token %d vs %d)", s, tok, rt);
+        } else {
+            compare(lg.data(), rl, tok, rt, "cached-prefix prefill");
+        }
+        last[s] = rt;   // both sides continue from the batch-1 model's token
     }
     EXPECT(cache.page_refs(cache.host_block_table(0)[0]) == 2, "shared page refs");
     bool threw = false;

@@ -2,14 +2,19 @@
 reference docs/runner_interface.md): a minimal scheduler loop owns the
 block allocator -- it allocates the prompt blocks, forks the blocks of a
 cached prefix (the third sequence reuses the first one's two full prompt
-blocks, num_cached_tokens = 32), allocates the next block when a sequence
-fills its last one, and is the only writer of generated_ids / last_token_id
-(post_step) -- while the Runner prefills and decodes.  Every sequence is
-checked against a batch-1 model of the same weights fed the same tokens:
-prefill logits bit-identical, decode logits within 2 % of the logit scale
-with differing tokens only at near-ties (the reference's acceptance rule,
-margin < 0.05).  Shared blocks keep their bytes throughout, and freeing
-every sequence returns every block."""
+blocks, num_cached_tokens = 32; the fourth is exactly those 32 tokens),
+allocates the next block when a sequence fills its last one, and is the
+only writer of generated_ids / last_token_id (post_step) -- while the Runner
+prefills and decodes, in both prefix modes: "share" recomputes every prompt
+(flash prefill; shared blocks' writes dropped), "full" forwards only the
+uncached suffix, attending to the cached prefix from the pages.  Every
+sequence is checked against a batch-1 model of the same weights fed the
+same tokens: prefill logits bit-identical where the same kernels run (every
+"share" prefill, "full" prefills without a cached prefix), within 2 % of the
+logit scale otherwise; decode logits within 2 %; differing greedy tokens
+only at near-ties (the reference's acceptance rule, margin < 0.05).  Shared
+blocks keep their bytes throughout, and freeing every sequence returns
+every block."""
 import numpy as np
 import pytest
 
@@ -33,22 +38,24 @@ def _close(got, ref, what):
         assert top2_margin(ref) < NEAR_TIE, f"{what}: greedy token differs outside a near-tie"
 
 
-def test_runner_with_prefix_sharing_matches_batch1_models():
+@pytest.mark.parametrize("mode", ["share", "full"])
+def test_runner_with_prefix_sharing_matches_batch1_models(mode):
     cfg = kvhp.LlamaConfig(2048, 512, 3, 8, 2, 64, 1024, 1e-5, 10000.0, 0)
     seed, max_ctx, steps = 33, 128, 20
     model = kvhp.LlamaModel(cfg, seed=seed, max_ctx=max_ctx)
-    run = rc.Runner(model, num_blocks=40)
+    run = rc.Runner(model, num_blocks=40, prefix_mode=mode)
     alloc = rc.BlockAllocator(40)
     rng = np.random.default_rng(808)
     p0 = rng.integers(0, cfg.vocab_size, 37).tolist()
     p1 = rng.integers(0, cfg.vocab_size, 21).tolist()
     p2 = p0[:32] + rng.integers(0, cfg.vocab_size, 9).tolist()
-    seqs = [rc.Sequence(prompt_ids=p) for p in (p0, p1, p2)]
+    p3 = p0[:32]
+    seqs = [rc.Sequence(prompt_ids=p) for p in (p0, p1, p2, p3)]
 
-    # scheduler: prompt blocks; sequence 2 hits sequence 0's cached prefix
+    # scheduler: prompt blocks; sequences 2 and 3 hit sequence 0's cached prefix
     for i, s in enumerate(seqs):
         n = len(s.prompt_ids)
-        if i == 2:
+        if i >= 2:
             s.block_table.physical_block_ids = [alloc.fork(b) for b in
                                                 seqs[0].block_table.physical_block_ids[:2]]
             s.num_cached_tokens = 32
@@ -56,14 +63,18 @@ def test_runner_with_prefix_sharing_matches_batch1_models():
             s.block_table.physical_block_ids.append(alloc.allocate())
         s.block_table.num_tokens = n
     shared = seqs[0].block_table.physical_block_ids[:2]
-    assert all(alloc.ref_counts[b] == 2 for b in shared)
+    assert all(alloc.ref_counts[b] == 3 for b in shared)
 
     singles = [kvhp.LlamaModel(cfg, seed=seed, max_ctx=max_ctx) for _ in seqs]
     pool = run.pool_view()
     for i, s in enumerate(seqs):
         tok = run.step(rc.ScheduledBatch(rc.BatchType.PREFILL, [s]))[0]
         rtok, rlg = singles[i].prefill(np.array(s.prompt_ids, np.int32))
-        assert tok == rtok and np.array_equal(s.last_logits.numpy(), rlg), f"prefill {i}"
+        if mode == "share" or s.num_cached_tokens == 0:
+            assert tok == rtok and np.array_equal(s.last_logits.numpy(), rlg), f"prefill {i}"
+        else:
+            _close(s.last_logits.numpy(), rlg, f"cached-prefix prefill {i}")
+            tok = rtok   # continue both sides from the same token
         assert s.block_table.num_tokens == len(s.prompt_ids)    # the runner leaves it
         s.generated_ids.append(tok)                             # post_step
         s.last_token_id = tok
