@@ -199,6 +199,9 @@ class Runner:
         # every sequence is checked before any is bumped, so a failed
         # assertion leaves the batch as it was
         for s in seqs:
+            if s.last_token_id < 0 and not s.generated_ids:
+                raise AssertionError("decode_step: a sequence without last_token_id or "
+                                     "generated_ids (the previous step's token)")
             write_pos = s.block_table.num_tokens     # = the bumped num_tokens - 1
             self._check_blocks(s, write_pos + 1, "decode_step")
             blk = s.block_table.physical_block_ids[write_pos // BLOCK_SIZE]
@@ -214,8 +217,7 @@ class Runner:
             ids = s.block_table.physical_block_ids
             tables[i, :len(ids)] = ids
         seq_lens = np.array([s.block_table.num_tokens for s in seqs], np.int32)
-        tokens = np.array([s.last_token_id if s.last_token_id >= 0 else
-                           (s.generated_ids[-1] if s.generated_ids else s.prompt_ids[-1])
+        tokens = np.array([s.last_token_id if s.last_token_id >= 0 else s.generated_ids[-1]
                            for s in seqs], np.int32)
         V = self.model.config.vocab_size
         with torch.inference_mode():

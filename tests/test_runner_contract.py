@@ -65,11 +65,14 @@ def test_decode_refuses_a_write_into_a_shared_block():
     # a second sequence shares the owner's first block and ends inside it
     other = rc.Sequence(prompt_ids=list(range(5)))
     other.block_table = rc.BlockTable([a.fork(owner.block_table.physical_block_ids[0])], 5)
+    with pytest.raises(AssertionError, match="last_token_id"):
+        r.decode_step([owner], a)                            # no token to feed yet
+    owner.last_token_id = other.last_token_id = 7
     with pytest.raises(AssertionError, match="shared"):
         r.decode_step([owner, other], a)
     assert owner.block_table.num_tokens == 20 and other.block_table.num_tokens == 5
     # a sequence at a block boundary without its next block
-    edge = rc.Sequence(prompt_ids=list(range(16)))
+    edge = rc.Sequence(prompt_ids=list(range(16)), last_token_id=3)
     edge.block_table = rc.BlockTable([a.allocate()], 16)
     with pytest.raises(AssertionError, match="blocks"):
         r.decode_step([edge], a)
