@@ -126,3 +126,24 @@ def test_host_validation_errors():
 def test_error_raises_in_binding():
     with pytest.raises(kvhp.KVHPError):
         kvhp._check(kvhp.load().kvhp_append_kv(None, None, None, None, 4, 0, 2, 16, 64, None))
+
+
+def test_header_is_plain_c(tmp_path):
+    """include/kvhp_c.h compiles as strict C11 (no C++ in the ABI) and a C
+    program links against libkvhp.so."""
+    import os
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no gcc")
+    src = tmp_path / "use_abi.c"
+    src.write_text('#include "kvhp_c.h"\n'
+                   'int main(void) { return kvhp_abi_version() == KVHP_ABI_VERSION ? 0 : 1; }\n')
+    inc = os.path.dirname(kvhp.HEADER_PATH)
+    libdir = os.path.dirname(kvhp.LIB_PATH)
+    subprocess.run([gcc, "-std=c11", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", inc,
+                    str(src), "-L", libdir, "-lkvhp", "-L/opt/rocm/lib", "-lamdhip64",
+                    "-Wl,-rpath," + libdir, "-Wl,--allow-shlib-undefined",
+                    "-o", str(tmp_path / "use_abi")], check=True)
+
