@@ -44,6 +44,7 @@ namespace kvhp {
 namespace {
 
 constexpr float kInitStd = 0.02f;
+constexpr int kShortSuffix = 32;  // cached-prefix suffixes up to this run as one batched step
 
 struct Layer {
     f16* attn_norm = nullptr;  // [H]
@@ -81,6 +82,8 @@ struct Model {
     int32_t* log = nullptr;    // [max_ctx] generated tokens
     int32_t* aux = nullptr;    // cached-prefix prefill: replicated block-table rows, lengths
     size_t aux_words = 0;
+    float* suffix_logits = nullptr;  // [kShortSuffix][V]: logits of a short cached-prefix prefill
+    int32_t* suffix_next = nullptr;  // [kShortSuffix]
     void* ws = nullptr;        // decode attention workspace
     size_t ws_bytes = 0;
     int prompt_len = 0;
@@ -215,16 +218,53 @@ int prefill_layers(Model& m, int n, const Pages& pg, void* s) {
 // Inputs of a cached-prefix prefill's attention, on the device: row r of
 // tables [rows][width] is the sequence's block-table row, lens[r] =
 // first + r + 1 (query row r sits at position first + r), start[0] = first.
-__global__ void suffix_rows_kernel(int32_t* tables, int32_t* lens, int32_t* start,
-                                   const int32_t* row, int rows, int width, int first) {
+__global__ void suffix_rows_kernel(int32_t* tables, int32_t* wtables, int32_t* lens,
+                                   int32_t* pos, int32_t* start, const int32_t* row,
+                                   const int32_t* wrow, int rows, int width, int first) {
     const int64_t total = (int64_t)rows * width;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x)
+         i += (int64_t)gridDim.x * blockDim.x) {
         tables[i] = row[i % width];
+        wtables[i] = wrow[i % width];
+    }
     for (int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; r < rows;
-         r += (int64_t)gridDim.x * blockDim.x)
+         r += (int64_t)gridDim.x * blockDim.x) {
         lens[r] = first + static_cast<int32_t>(r) + 1;
+        pos[r] = first + static_cast<int32_t>(r);
+    }
     if (blockIdx.x == 0 && threadIdx.x == 0) start[0] = first;
+}
+
+// Device inputs of a cached-prefix prefill of `rows` suffix rows (in m.aux):
+// replicated read and write block-table rows, lengths, positions, start.
+struct SuffixRows {
+    int32_t *tables, *wtables, *lens, *pos, *start;
+};
+
+int suffix_rows(Model& m, const Pages& pg, const int32_t* write_bt, int first, int rows,
+                hipStream_t s, SuffixRows& out) {
+    const size_t words = 2 * (size_t)rows * pg.max_pages + 2 * (size_t)rows + 1;
+    if (m.aux_words < words) {
+        KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(aux)");
+        if (m.aux) {
+            for (auto& p : m.allocs)
+                if (p == m.aux) p = nullptr;
+            (void)hipFree(m.aux);
+            m.aux = nullptr;
+        }
+        KVHP_TRY(alloc_n(m, words, &m.aux));
+        m.aux_words = words;
+    }
+    out.tables = m.aux;
+    out.wtables = out.tables + (size_t)rows * pg.max_pages;
+    out.lens = out.wtables + (size_t)rows * pg.max_pages;
+    out.pos = out.lens + rows;
+    out.start = out.pos + rows;
+    const int64_t blocks = std::min<int64_t>(((int64_t)rows * pg.max_pages + 255) / 256, 1024);
+    hipLaunchKernelGGL(suffix_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,
+                       out.tables, out.wtables, out.lens, out.pos, out.start, pg.bt, write_bt,
+                       rows, pg.max_pages, first);
+    return check_launch("suffix_rows");
 }
 
 // "Full" prefix mode: only prompt positions [first, n) run through the
@@ -239,26 +279,11 @@ int prefill_suffix_layers(Model& m, int first, int n, const Pages& pg, const int
     const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
     const int F = c.ffn_size, NQKV = (Hq + 2 * Hkv) * D;
     const int S = n - first;
-    const size_t words = (size_t)S * pg.max_pages + S + 1;
-    if (m.aux_words < words) {
-        KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(aux)");
-        if (m.aux) {
-            for (auto& p : m.allocs)
-                if (p == m.aux) p = nullptr;
-            (void)hipFree(m.aux);
-            m.aux = nullptr;
-        }
-        KVHP_TRY(alloc_n(m, words, &m.aux));
-        m.aux_words = words;
-    }
-    int32_t* tables = m.aux;
-    int32_t* lens = tables + (size_t)S * pg.max_pages;
-    int32_t* start = lens + S;
-    const int64_t blocks = std::min<int64_t>(((int64_t)S * pg.max_pages + 255) / 256, 1024);
-    hipLaunchKernelGGL(suffix_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,
-                       tables, lens, start, pg.bt, S, pg.max_pages, first);
-    KVHP_TRY(check_launch("suffix_rows"));
-    const Pages rows_pg{pg.base, pg.num_pages, tables, pg.max_pages};
+    SuffixRows sr{};
+    KVHP_TRY(suffix_rows(m, pg, write_bt, first, S, s, sr));
+    int32_t* lens = sr.lens;
+    int32_t* start = sr.start;
+    const Pages rows_pg{pg.base, pg.num_pages, sr.tables, pg.max_pages};
     KVHP_TRY(kvhp_embedding(m.tokens + first, m.embed, m.hidden, S, H, c.vocab_size, s));
     for (int l = 0; l < c.num_layers; ++l) {
         const Layer& L = m.layers[l];
@@ -288,7 +313,12 @@ int prefill_suffix_layers(Model& m, int first, int n, const Pages& pg, const int
 // SwiGLU launches.
 int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                 const int32_t* positions, const int32_t* seq_lens, int max_seq_len,
-                float* logits, int32_t* next, void* s) {
+                float* logits, int32_t* next, void* s, const int32_t* write_bt = nullptr) {
+    // K/V appends go through write_bt when given (rows [B][max_pages] with
+    // shared pages -1), reads through pg.bt; only the fused paths take it
+    KVHP_REQUIRE(write_bt == nullptr || B <= 32, KVHP_ERR_INVALID,
+                 "decode_rows: a separate write table needs batch <= 32");
+    const int32_t* wbt = write_bt ? write_bt : pg.bt;
     const kvhp_llama_config& c = m.c;
     const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
     const int F = c.ffn_size, NQKV = (Hq + 2 * Hkv) * D;
@@ -300,7 +330,7 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
             KVHP_TRY(rmsnorm_qkv_rope_append_at(L.w_qkv, m.hidden, L.attn_norm, c.rms_eps,
                                                 positions, c.rope_theta, m.q,
                                                 layer_pool(m, pg, l, 0), layer_pool(m, pg, l, 1),
-                                                pg.bt, pg.max_pages, pg.num_pages, Hq, Hkv, D, H,
+                                                wbt, pg.max_pages, pg.num_pages, Hq, Hkv, D, H,
                                                 static_cast<hipStream_t>(s)));
             const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
             KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, seq_lens, m.attn, 1, Hq, Hkv, D,
@@ -321,7 +351,7 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
             const Layer& L = m.layers[l];
             KVHP_TRY(kvhp_rmsnorm_qkv_rope_append_rows(
                 L.w_qkv, m.hidden, L.attn_norm, c.rms_eps, positions, c.rope_theta, m.q,
-                layer_pool(m, pg, l, 0), layer_pool(m, pg, l, 1), pg.bt, pg.max_pages,
+                layer_pool(m, pg, l, 0), layer_pool(m, pg, l, 1), wbt, pg.max_pages,
                 pg.num_pages, Hq, Hkv, D, H, B, s));
             const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
             KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, seq_lens, m.attn, B, Hq, Hkv, D,
@@ -470,6 +500,8 @@ extern "C" int kvhp_llama_create(const kvhp_llama_config* cfg, uint64_t seed, in
     KVHP_TRY(alloc_n(*m, S, &m->tokens));
     KVHP_TRY(alloc_n(*m, 4, &m->state));
     KVHP_TRY(alloc_n(*m, S, &m->log));
+    KVHP_TRY(alloc_n(*m, (size_t)kShortSuffix * V, &m->suffix_logits));
+    KVHP_TRY(alloc_n(*m, kShortSuffix, &m->suffix_next));
     // K = hidden (q/k/v, gate/up, LM head), Hq*D (o) and ffn (down): 256*n
     // with n <= 8, or 352*n with n <= 16 for the down projection
     auto k256 = [](int K) { return K % 256 == 0 && K / 256 <= 8; };
@@ -633,21 +665,36 @@ int prefill_pages(void* model, const int32_t* tokens, int n, int first, void* po
     const Pages pg{static_cast<f16*>(pool), num_pages, block_table, max_pages};
     KVHP_HIP(hipMemcpyAsync(m.tokens, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s),
              "hipMemcpyAsync(tokens)");
-    if (first == 0)
-        KVHP_TRY(prefill_layers(m, n, pg, s));
-    else
-        KVHP_TRY(prefill_suffix_layers(m, first, n, pg, write_table ? write_table : block_table,
-                                       s));
-    const int H = c.hidden_size;
-    KVHP_TRY(kvhp_rmsnorm_gemv(m.lm_head, m.hidden + (size_t)(n - first - 1) * H, m.final_norm,
-                               c.rms_eps, nullptr, m.logits, c.vocab_size, H, s));
-    KVHP_TRY(kvhp_argmax_rows(m.logits, 1, c.vocab_size, m.state + 3, s));
+    const int S = n - first;
+    const float* last_logits = m.logits;
+    const int32_t* last_tok = m.state + 3;
+    if (first > 0 && S <= kShortSuffix && (S == 1 || m.rows_ok)) {
+        // a short suffix is one batched decode step: row r at position
+        // first + r appends its K/V, then attends over first + r + 1 keys
+        SuffixRows sr{};
+        KVHP_TRY(suffix_rows(m, pg, write_table ? write_table : block_table, first, S, s, sr));
+        const Pages rows_pg{pg.base, pg.num_pages, sr.tables, pg.max_pages};
+        KVHP_TRY(decode_rows(m, m.tokens + first, S, rows_pg, sr.pos, sr.lens, n,
+                             m.suffix_logits, m.suffix_next, s, sr.wtables));
+        last_logits = m.suffix_logits + (size_t)(S - 1) * c.vocab_size;
+        last_tok = m.suffix_next + S - 1;
+    } else {
+        if (first == 0)
+            KVHP_TRY(prefill_layers(m, n, pg, s));
+        else
+            KVHP_TRY(prefill_suffix_layers(m, first, n, pg,
+                                           write_table ? write_table : block_table, s));
+        const int H = c.hidden_size;
+        KVHP_TRY(kvhp_rmsnorm_gemv(m.lm_head, m.hidden + (size_t)(S - 1) * H, m.final_norm,
+                                   c.rms_eps, nullptr, m.logits, c.vocab_size, H, s));
+        KVHP_TRY(kvhp_argmax_rows(m.logits, 1, c.vocab_size, m.state + 3, s));
+    }
     if (logits_out)
-        KVHP_HIP(hipMemcpyAsync(logits_out, m.logits, (size_t)c.vocab_size * 4,
+        KVHP_HIP(hipMemcpyAsync(logits_out, last_logits, (size_t)c.vocab_size * 4,
                                 hipMemcpyDeviceToHost, s),
                  "hipMemcpyAsync(logits)");
     int32_t tok = 0;
-    KVHP_HIP(hipMemcpyAsync(&tok, m.state + 3, 4, hipMemcpyDeviceToHost, s),
+    KVHP_HIP(hipMemcpyAsync(&tok, last_tok, 4, hipMemcpyDeviceToHost, s),
              "hipMemcpyAsync(token)");
     KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(prefill)");
     if (next_token) *next_token = tok;

@@ -237,6 +237,45 @@ def test_paged_runner_single_sequence_step_is_the_batch1_step():
     model.close()
 
 
+@pytest.mark.parametrize("suffix", [1, 7, 32, 33, 70])
+def test_cached_prefix_prefill_matches_full_prefill(suffix):
+    """kvhp_llama_prefill_cached over a prefix whose K/V another prefill
+    wrote: up to 32 suffix rows run as one batched decode step (one row on
+    the batch-1 kernels), longer suffixes layer by layer with a batched
+    decode-attention call; either way the last position's logits match the
+    whole-prompt prefill within 2 % of the scale (near-tie rule for the
+    token), the prefix pages keep their bytes and the suffix K/V land in the
+    following pages."""
+    cfg = _cfg()
+    L, Hkv, D, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
+    cached, max_pages = 48, 10
+    n = cached + suffix
+    P = 2 * max_pages
+    model = kvhp.LlamaModel(cfg, seed=77, max_ctx=160)
+    rng = np.random.default_rng(suffix)
+    prompt = rng.integers(0, V, n).astype(np.int32)
+    pool = torch.zeros(L * 2 * Hkv * P * PAGE * D, dtype=torch.float16, device="cuda")
+    pool5 = pool.view(L, 2, Hkv, P, PAGE, D)
+    perm = rng.permutation(P).astype(np.int32)
+    bt_a = torch.from_numpy(perm[:max_pages]).cuda()             # whole-prompt sequence
+    bt_b = torch.from_numpy(np.concatenate([perm[:3], perm[max_pages:2 * max_pages - 3]])).cuda()
+    _, ref = model.prefill_paged(prompt, pool, P, bt_a, max_pages)
+    torch.cuda.synchronize()
+    prefix = pool5[:, :, :, perm[:3]].clone()
+    wt = bt_b.clone()
+    wt[:3] = -1                                                   # shared prefix pages
+    tok, lg = model.prefill_cached(prompt, cached, pool, P, bt_b, max_pages, write_table=wt)
+    torch.cuda.synchronize()
+    _close(lg, ref, f"suffix {suffix}")
+    assert torch.equal(pool5[:, :, :, perm[:3]], prefix)
+    # the suffix K/V: B's pages against A's, position by position
+    for t in range(cached, n, max(1, suffix // 5)):
+        a = pool5[:, :, :, int(bt_a[t // PAGE]), t % PAGE].float()
+        b = pool5[:, :, :, int(bt_b[t // PAGE]), t % PAGE].float()
+        assert float((a - b).abs().max()) <= 0.02 * max(float(a.abs().max()), 1.0), t
+    model.close()
+
+
 def test_paged_runner_argument_errors():
     cfg = _cfg()
     model = kvhp.LlamaModel(cfg, seed=3, max_ctx=32)
