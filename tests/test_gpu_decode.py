@@ -194,6 +194,33 @@ def test_balanced_split_list_corners(case):
     assert_attn_close(got, ref, case)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_balanced_split_list_random_batches(seed):
+    """Randomised batches through the automatic split mode: batch sizes from
+    8 (the smallest balanced batch) to 200, length distributions from
+    uniform to heavy-tailed (a few long sequences among many short ones),
+    with empty sequences, D = 64 or 128 and G = 4 or 8, fused append on
+    every other case; every output against the oracle."""
+    rng = np.random.default_rng(1000 + seed)
+    b = int(rng.choice([8, 9, 16, 31, 64, 200]))
+    # host K/V are dense [b][max len]: wide heads only for the smaller batches
+    hq, hkv, d = (32, 8, 128) if seed % 2 and b <= 31 else (16, 2, 64)
+    kind = seed % 3
+    if kind == 0:
+        lens = rng.integers(0, 3000, size=b)
+    elif kind == 1:                       # heavy tail: most short, a few long
+        lens = rng.integers(0, 64, size=b)
+        lens[rng.choice(b, size=max(1, b // 10), replace=False)] = rng.integers(2000, 6000)
+    else:                                 # near-equal lengths around one value
+        lens = rng.integers(1500, 1600, size=b)
+    lens[rng.random(b) < 0.1] = 0
+    lens = lens.astype(np.int32)
+    note(f"balanced random seed={seed}: B={b} kind={kind} D={d} G={hq // hkv} "
+         f"max={int(lens.max())} sum={int(lens.sum())}")
+    got, ref = _paged_case(rng, b, lens, hq, hkv, d, with_append=True, fused=seed % 2 == 0)
+    assert_attn_close(got, ref, f"seed {seed}")
+
+
 @pytest.mark.parametrize("fused", [False, True])
 def test_config3_paged_decode_full_size(fused):
     """BASELINE config 3 at full size: 32 sequences with seeded lengths in
