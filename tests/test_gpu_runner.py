@@ -105,3 +105,71 @@ def test_runner_with_prefix_sharing_matches_batch1_models(mode):
     for m in singles:
         m.close()
     model.close()
+
+
+def test_serving_simulation_with_arrivals_departures_and_prefix_hits():
+    """A continuous-batching loop in miniature: each step may admit a new
+    sequence (a third of them reuse the full blocks of a live sequence's
+    prompt prefix, in the "full" prefix mode) and retire finished ones, then
+    decodes every live sequence in one batch whose membership changes from
+    step to step.  Every logit vector is checked against that sequence's own
+    batch-1 model fed the same tokens; blocks are freed as sequences finish
+    and none leak."""
+    cfg = kvhp.LlamaConfig(1024, 256, 2, 4, 2, 64, 512, 1e-5, 10000.0, 0)
+    seed, num_blocks = 44, 96
+    model = kvhp.LlamaModel(cfg, seed=seed, max_ctx=160)
+    run = rc.Runner(model, num_blocks=num_blocks, prefix_mode="full")
+    alloc = rc.BlockAllocator(num_blocks)
+    rng = np.random.default_rng(2024)
+    live, singles, budget = [], {}, {}
+    admitted = 0
+    for step in range(30):
+        if admitted < 10 and rng.random() < 0.5:
+            prompt = rng.integers(0, cfg.vocab_size, int(rng.integers(5, 60))).tolist()
+            s = rc.Sequence(prompt_ids=prompt)
+            donors = [d for d in live if len(d.prompt_ids) >= 16]
+            if donors and admitted % 3 == 2:          # prefix hit on a live sequence
+                d = donors[int(rng.integers(len(donors)))]
+                nb = len(d.prompt_ids) // 16
+                s.prompt_ids = d.prompt_ids[:16 * nb] + prompt[:int(rng.integers(0, 20))]
+                s.block_table.physical_block_ids = [alloc.fork(b) for b in
+                                                    d.block_table.physical_block_ids[:nb]]
+                s.num_cached_tokens = 16 * nb
+            n = len(s.prompt_ids)
+            while len(s.block_table.physical_block_ids) * 16 < n:
+                s.block_table.physical_block_ids.append(alloc.allocate())
+            s.block_table.num_tokens = n
+            ref = kvhp.LlamaModel(cfg, seed=seed, max_ctx=160)
+            tok = run.prefill(s)
+            rtok, rlg = ref.prefill(np.array(s.prompt_ids, np.int32))
+            _close(s.last_logits.numpy(), rlg, f"admit {admitted} at step {step}")
+            s.generated_ids.append(rtok)
+            s.last_token_id = rtok
+            singles[id(s)] = ref
+            budget[id(s)] = int(rng.integers(3, 15))
+            live.append(s)
+            admitted += 1
+        if not live:
+            continue
+        for s in live:
+            if s.block_table.num_tokens % 16 == 0:
+                s.block_table.physical_block_ids.append(alloc.allocate())
+        toks = run.decode_step(live, alloc)
+        for s, t in zip(live, toks):
+            _, rlg = singles[id(s)].decode_step(s.last_token_id)
+            _close(s.last_logits.numpy(), rlg, f"step {step}")
+            s.generated_ids.append(t)
+            s.last_token_id = t
+            budget[id(s)] -= 1
+        for s in [s for s in live if budget[id(s)] <= 0]:   # retire
+            for b in s.block_table.physical_block_ids:
+                alloc.free(b)
+            singles.pop(id(s)).close()
+            live.remove(s)
+    for s in live:
+        for b in s.block_table.physical_block_ids:
+            alloc.free(b)
+        singles.pop(id(s)).close()
+    assert admitted >= 6
+    assert alloc.num_free() == num_blocks and not alloc.ref_counts.any()
+    model.close()
