@@ -346,6 +346,36 @@ def test_decode_caller_workspace_reuse_and_empty_sequences():
         assert np.all(got[np.array(lens) == 0] == 0)
 
 
+@pytest.mark.parametrize("balanced", [False, True])
+def test_decode_ignores_stale_workspace_slots(balanced):
+    """The merge reads every split slot of a sequence before it knows how
+    many the sequence used; slots it did not use may hold anything.  A
+    caller workspace filled with NaN bytes (and one filled with huge values)
+    must not change a single output: short sequences use few of the 32
+    slots, one uses many.  Balanced: a batch of 12 in the automatic split
+    mode; otherwise an explicit 32-way split."""
+    import torch
+    rng = np.random.default_rng(77 + balanced)
+    hq, hkv, d, cap = 32, 8, 128, 4096
+    lens = [4096, 40, 1, 300, 0, 2000] * (2 if balanced else 1)
+    b = len(lens)
+    splits = 0 if balanced else 32
+    ws_bytes = kvhp.decode_workspace_bytes(b, hq, hkv, d, cap, splits)
+    q = oracle.normal_f16(rng, (b, hq, d))
+    kc, vc = oracle.normal_f16(rng, (b, hkv, cap, d)), oracle.normal_f16(rng, (b, hkv, cap, d))
+    ref = oracle.decode_attention(q.astype(np.float32), kc.astype(np.float32),
+                                  vc.astype(np.float32), np.array(lens, np.int32), hq, hkv, d)
+    outs = []
+    for fill in (0xFF, 0x7F):          # NaN bytes; 3.4e38-ish floats
+        ws = torch.full((ws_bytes,), fill, dtype=torch.uint8, device="cuda")
+        note(f"stale workspace fill=0x{fill:02x} balanced={balanced}")
+        got = _run_contig(q, kc, vc, lens, hq, hkv, d, cap, splits, ws)
+        assert np.isfinite(got).all(), f"fill 0x{fill:02x}: non-finite output"
+        assert_attn_close(got, ref, f"fill 0x{fill:02x}")
+        outs.append(got)
+    assert np.array_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("hq,hkv,d,tiles", [(32, 8, 128, 1), (32, 4, 64, 1), (12, 4, 96, 1),
                                             (32, 8, 128, 10), (32, 4, 64, 10)])
 def test_paged_append_decode_matches_separate_calls(hq, hkv, d, tiles):
