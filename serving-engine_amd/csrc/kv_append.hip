@@ -9,6 +9,8 @@
 // A scalar (2-byte) variant handles head dims that are not multiples of 8.
 #include "kvhp_internal.h"
 
+#include <algorithm>
+
 namespace kvhp {
 
 namespace {
@@ -128,6 +130,53 @@ gather_paged_kernel(const f16* __restrict__ pool_k, const f16* __restrict__ pool
     }
 }
 
+// Paged gather by pages: one wave per (sequence, KV head, page) moves the
+// page's 16 rows of K and of V (32*D contiguous bytes each, in the pool and
+// in the output alike), CPL = D/32 16-byte chunks per lane and tensor, all
+// loads of both tensors in flight before the stores; one block-table
+// lookup per page.  Rows at or past seq_lens[b], and pages outside the
+// pool, are written as zeros; rows past max_len are not written.
+template <int CPL>
+__global__ void __launch_bounds__(kCopyThreads)
+gather_pages_kernel(const f16* __restrict__ pool_k, const f16* __restrict__ pool_v,
+                    const int32_t* __restrict__ block_tables, int max_pages,
+                    const int32_t* __restrict__ seq_lens, int64_t n_units, int pages_per_seq,
+                    int max_len, int num_kv_heads, int num_pages, f16* __restrict__ out_k,
+                    f16* __restrict__ out_v) {
+    constexpr int D = 32 * CPL;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    for (int64_t u = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; u < n_units;
+         u += nwaves) {
+        const int p = static_cast<int>(u % pages_per_seq);
+        const int64_t bh = u / pages_per_seq;          // b * Hkv + h
+        const int h = static_cast<int>(bh % num_kv_heads);
+        const int b = static_cast<int>(bh / num_kv_heads);
+        const int L = seq_lens[b];
+        int pid = -1;
+        if (kPage * p < L && p < max_pages) pid = block_tables[(int64_t)b * max_pages + p];
+        const bool ok = pid >= 0 && pid < num_pages;
+        const int64_t src = ok ? ((int64_t)h * num_pages + pid) * kPage * D : 0;
+        const int64_t dst = (bh * max_len + (int64_t)kPage * p) * D;
+        half8 kx[CPL], vx[CPL];
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + kWave * i;            // chunk of the page: row 8c / D
+            const bool valid = ok && kPage * p + (8 * c) / D < L;
+            kx[i] = valid ? load_half8_stream(pool_k + src + 8 * c) : half8{};
+            vx[i] = valid ? load_half8_stream(pool_v + src + 8 * c) : half8{};
+        }
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + kWave * i;
+            if (kPage * p + (8 * c) / D < max_len) {
+                store_half8(out_k + dst + 8 * c, kx[i]);
+                store_half8(out_v + dst + 8 * c, vx[i]);
+            }
+        }
+    }
+}
+
 // Grid for a grid-stride copy: enough waves to cover HBM latency on 256 CUs,
 // capped so very large copies loop instead of launching millions of groups.
 inline unsigned copy_grid(int64_t n_items) {
@@ -228,6 +277,22 @@ extern "C" int kvhp_paged_gather_kv(const void* pool_k, const void* pool_v,
     const int cpr = head_dim / vw;
     const int64_t n = (int64_t)batch * num_kv_heads * max_len * cpr;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (vec && (head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256)) {
+        const int pps = (max_len + kPage - 1) / kPage;
+        const int64_t units = (int64_t)batch * num_kv_heads * pps;
+        const int64_t blocks = std::min<int64_t>((units + 3) / 4, 256 * 64);
+        const dim3 grid(static_cast<unsigned>(std::max<int64_t>(blocks, 1)));
+        auto args = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(kCopyThreads), 0, s, (const f16*)pool_k,
+                               (const f16*)pool_v, block_tables, max_pages, seq_lens, units, pps,
+                               max_len, num_kv_heads, num_pages, (f16*)out_k, (f16*)out_v);
+        };
+        if (head_dim == 32) args(gather_pages_kernel<1>);
+        else if (head_dim == 64) args(gather_pages_kernel<2>);
+        else if (head_dim == 128) args(gather_pages_kernel<4>);
+        else args(gather_pages_kernel<8>);
+        return check_launch("paged_gather_kv");
+    }
     if (vec)
         hipLaunchKernelGGL(gather_paged_kernel<8>, dim3(copy_grid(n)), dim3(kCopyThreads),
                            0, s, (const f16*)pool_k, (const f16*)pool_v, block_tables,

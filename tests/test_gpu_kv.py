@@ -89,7 +89,8 @@ def test_paged_append_drops_out_of_range():
     del torch
 
 
-@pytest.mark.parametrize("b,hkv,d,maxlen", [(3, 2, 64, 100), (8, 8, 128, 700), (2, 1, 40, 33)])
+@pytest.mark.parametrize("b,hkv,d,maxlen", [(3, 2, 64, 100), (8, 8, 128, 700), (2, 1, 40, 33),
+                                            (4, 3, 32, 50), (2, 2, 256, 90)])
 def test_paged_gather_bit_exact(b, hkv, d, maxlen):
     import torch
     rng = np.random.default_rng(300 + b)
@@ -106,6 +107,30 @@ def test_paged_gather_bit_exact(b, hkv, d, maxlen):
     ek, ev = oracle.paged_gather(pool_k.view(np.uint16), pool_v.view(np.uint16), bt, lens, maxlen)
     assert np.array_equal(from_gpu(ok).view(np.uint16), ek)
     assert np.array_equal(from_gpu(ov).view(np.uint16), ev)
+
+
+@pytest.mark.parametrize("d", [64, 40])
+def test_paged_gather_invalid_page_ids_read_as_zero(d):
+    """Block-table entries outside [0, P) (-1, P, a huge id) gather zeros for
+    their rows, on the page-per-wave kernel (D = 64) and the per-chunk one
+    (D = 40); rows past the length are zero, past max_len unwritten."""
+    import torch
+    rng = np.random.default_rng(90 + d)
+    hkv, P, maxlen = 2, 6, 70
+    bt = np.array([[0, -1, 3, 9], [5, 2, 1 << 30, 4]], np.int32)
+    lens = np.array([64, 57], np.int32)
+    pool_k = _src(rng, (hkv, P, 16, d))
+    pool_v = _src(rng, (hkv, P, 16, d))
+    note(f"paged_gather invalid ids D={d}")
+    ok = torch.full((2, hkv, maxlen, d), 7.0, dtype=torch.float16, device="cuda")
+    ov = torch.full_like(ok, 7.0)
+    kvhp.paged_gather_kv(to_gpu_f16(pool_k), to_gpu_f16(pool_v), to_gpu(bt), to_gpu(lens),
+                         maxlen, ok, ov)
+    sync()
+    ek, ev = oracle.paged_gather(pool_k.view(np.uint16), pool_v.view(np.uint16), bt, lens, maxlen)
+    assert np.array_equal(from_gpu(ok).view(np.uint16), ek)
+    assert np.array_equal(from_gpu(ov).view(np.uint16), ev)
+    assert not ek[0, :, 16:32].any() and not ek[1, :, 32:48].any()
 
 
 def test_config3_scale_append_gather_round_trip():
