@@ -276,6 +276,50 @@ def test_cached_prefix_prefill_matches_full_prefill(suffix):
     model.close()
 
 
+def test_paged_runner_qwen_shapes_use_the_fallback_projections():
+    """The reference runner's own model shapes (docs/runner_interface.md:
+    hidden 896, 14 query / 2 KV heads -- G = 7 --, head_dim 64; here 2
+    layers, FFN 4864, vocab 3000): hidden 896 is not a multiple of 256, so
+    batches of 2..32 take the library-GEMM path and a batch of one the
+    generic batch-1 GEMVs.  Three sequences, prefill and four decode steps,
+    against batch-1 models of the same weights (2 % of the logit scale,
+    near-tie rule)."""
+    cfg = kvhp.LlamaConfig(3000, 896, 2, 14, 2, 64, 4864, 1e-6, 1000000.0, 0)
+    L, Hkv, D, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
+    P, max_pages = 24, 6
+    rng = np.random.default_rng(896)
+    model = kvhp.LlamaModel(cfg, seed=9, max_ctx=96)
+    pool = torch.zeros(L * 2 * Hkv * P * PAGE * D, dtype=torch.float16, device="cuda")
+    bt = torch.from_numpy(rng.permutation(P)[:3 * max_pages].astype(np.int32).reshape(3, max_pages)).cuda()
+    prompts = [rng.integers(0, V, n).astype(np.int32) for n in (30, 17, 52)]
+    singles = [kvhp.LlamaModel(cfg, seed=9, max_ctx=96) for _ in prompts]
+    toks = []
+    for i, pr in enumerate(prompts):
+        tok, lg = model.prefill_paged(pr, pool, P, bt[i], max_pages)
+        rtok, rlg = singles[i].prefill(pr)
+        assert tok == rtok and np.array_equal(lg, rlg), f"prefill {i}"
+        toks.append(tok)
+    seq = [len(p) for p in prompts]
+    for B in (3, 1):                      # library GEMMs, then the batch-1 kernels
+        for step in range(2):
+            logits = torch.empty(B, V, dtype=torch.float32, device="cuda")
+            nxt = torch.empty(B, dtype=torch.int32, device="cuda")
+            pos = torch.tensor(seq[:B], dtype=torch.int32, device="cuda")
+            model.decode_paged(torch.tensor(toks[:B], dtype=torch.int32, device="cuda"), pool, P,
+                               bt[:B].contiguous(), max_pages, pos, pos + 1, max(seq[:B]) + 1,
+                               logits, nxt)
+            torch.cuda.synchronize()
+            got = logits.cpu().numpy()
+            for b in range(B):
+                _, rlg = singles[b].decode_step(toks[b])
+                _close(got[b], rlg, f"B={B} step {step} sequence {b}")
+                toks[b] = int(nxt[b].item())
+                seq[b] += 1
+    for m in singles:
+        m.close()
+    model.close()
+
+
 def test_paged_runner_argument_errors():
     cfg = _cfg()
     model = kvhp.LlamaModel(cfg, seed=3, max_ctx=32)
