@@ -342,7 +342,10 @@ decode_splitk_kernel(const DecodeArgs a) {
 
     half8 kbuf[2][NVL];    // [ring slot][load]: whole rows, as V
     half8 vbuf[NVL];
-    const uint32_t kss = static_cast<uint32_t>(ssk) * 2u;  // row pitch, bytes
+    // Row pitch in bytes.  view_fast_ok admits stride_s < 2^26 halfs, so a
+    // row offset inside a page, at most 15 pitches, stays below 2^31: a full
+    // 32-bit multiply (a 24-bit one would drop the pitch's high bits).
+    const uint32_t kss = static_cast<uint32_t>(ssk) * 2u;
     const uint32_t vss = static_cast<uint32_t>(ssv) * 2u;
 
     // K and V are fetched the same way: lane (vrow, vdim) loads 16 bytes of
@@ -358,7 +361,7 @@ decode_splitk_kernel(const DecodeArgs a) {
 #pragma unroll
             for (int j = t * (kPage / RPL); j < (t + 1) * (kPage / RPL); ++j) {
                 const int s0 = ((RPL * j) & (kPage - 1)) + vrow;
-                const uint32_t off = __umul24(static_cast<uint32_t>(min(s0, lim)), kss) + 2u * vdim;
+                const uint32_t off = static_cast<uint32_t>(min(s0, lim)) * kss + 2u * vdim;
                 kbuf[S][j] = load_half8_stream(reinterpret_cast<const f16*>(pb + off));
             }
         }
@@ -371,7 +374,7 @@ decode_splitk_kernel(const DecodeArgs a) {
 #pragma unroll
             for (int j = t * (kPage / RPL); j < (t + 1) * (kPage / RPL); ++j) {
                 const int s0 = ((RPL * j) & (kPage - 1)) + vrow;
-                const uint32_t off = __umul24(static_cast<uint32_t>(min(s0, lim)), vss) + 2u * vdim;
+                const uint32_t off = static_cast<uint32_t>(min(s0, lim)) * vss + 2u * vdim;
                 vbuf[j] = load_half8_stream(reinterpret_cast<const f16*>(pb + off));
             }
         }

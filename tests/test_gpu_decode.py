@@ -424,3 +424,38 @@ def test_paged_append_decode_matches_separate_calls(hq, hkv, d, tiles):
     assert torch.equal(pk1, pk2) and torch.equal(pv1, pv2), "pools differ"
     assert torch.equal(out1, out2), "outputs differ"
     assert not torch.equal(pk2, pool_k), "nothing was appended"
+
+
+@pytest.mark.parametrize("stride_s", [(1 << 23) + 64, (1 << 24) + 8])
+def test_decode_row_pitch_beyond_24_bits(stride_s):
+    """A strided view whose row pitch needs more than 24 bits (stride_s
+    >= 2^23 halfs, still inside the fast kernel's stride_s < 2^26): the
+    split kernel's in-page row offsets must keep the pitch's high bits.  L=17
+    rows of one KV head (G=4, D=128), each row stride_s halfs apart, rows 1 and
+    16 of each page distinct, against the oracle."""
+    import torch
+    rng = np.random.default_rng(stride_s % 1000)
+    hq, hkv, d, L = 4, 1, 128, 17
+    q = oracle.normal_f16(rng, (1, hq, d))
+    rows_k = oracle.normal_f16(rng, (L, d))
+    rows_v = oracle.normal_f16(rng, (L, d))
+    n = (L - 1) * stride_s + d
+    note(f"decode row pitch {stride_s} halfs ({n * 2 / 2**20:.0f} MiB per tensor)")
+    kt = torch.zeros(n, dtype=torch.float16, device="cuda")
+    vt = torch.zeros(n, dtype=torch.float16, device="cuda")
+    idx = (torch.arange(L, device="cuda")[:, None] * stride_s +
+           torch.arange(d, device="cuda")[None, :]).reshape(-1)
+    kt[idx] = to_gpu_f16(rows_k).reshape(-1)
+    vt[idx] = to_gpu_f16(rows_v).reshape(-1)
+    kview = kvhp.strided_view(kt, 0, 0, stride_s)
+    vview = kvhp.strided_view(vt, 0, 0, stride_s)
+    out = torch.full((1, hq, d), float("nan"), dtype=torch.float16, device="cuda")
+    kvhp.decode_attention(to_gpu_f16(q), kview, vview, to_gpu(np.array([L], np.int32)), out,
+                          hq, hkv, d, L)
+    sync()
+    ref = oracle.decode_attention(q.astype(np.float32), rows_k[None, None].astype(np.float32),
+                                  rows_v[None, None].astype(np.float32),
+                                  np.array([L], np.int32), hq, hkv, d)
+    assert_attn_close(from_gpu(out).astype(np.float32), ref, f"stride_s={stride_s}")
+    del kt, vt
+    torch.cuda.empty_cache()
