@@ -84,8 +84,10 @@ struct Model {
     size_t aux_words = 0;
     float* suffix_logits = nullptr;  // [kShortSuffix][V]: logits of a short cached-prefix prefill
     int32_t* suffix_next = nullptr;  // [kShortSuffix]
-    void* ws = nullptr;        // decode attention workspace
+    void* ws = nullptr;        // decode attention workspace of the batch-1 step
     size_t ws_bytes = 0;
+    void* ws_rows = nullptr;   // decode attention workspace of the batched paths (grows)
+    size_t ws_rows_bytes = 0;
     int prompt_len = 0;
     bool rows_ok = false;      // batched projections fit the skinny-GEMM kernels
     hipGraph_t graph = nullptr;
@@ -122,6 +124,40 @@ int alloc_n(Model& m, size_t n, T** out) {
         const int rc_ = (expr);   \
         if (rc_) return rc_;      \
     } while (0)
+
+// Replace the model-owned buffer *p (of *cap elements) by one of n elements
+// once the stream's earlier work is done.  On failure *p is null and *cap 0.
+template <typename T>
+int regrow(Model& m, T** p, size_t* cap, size_t n, hipStream_t s) {
+    KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(regrow)");
+    if (*p) {
+        for (auto& a : m.allocs)
+            if (a == *p) a = nullptr;
+        (void)hipFree(*p);
+        *p = nullptr;
+    }
+    *cap = 0;
+    KVHP_TRY(alloc_n(m, n, p));
+    *cap = n;
+    return KVHP_OK;
+}
+
+// Decode-attention workspace for B sequences of up to max_seq_len keys,
+// owned by the model (not the library's per-device buffer), so that models
+// on different streams never share split partials.
+int rows_workspace(Model& m, int B, int max_seq_len, hipStream_t s, void** ws, size_t* bytes) {
+    const kvhp_llama_config& c = m.c;
+    const size_t need = kvhp_decode_workspace_bytes(B, c.num_q_heads, c.num_kv_heads, c.head_dim,
+                                                    max_seq_len, 0);
+    if (need > m.ws_rows_bytes) {
+        char* p = static_cast<char*>(m.ws_rows);
+        KVHP_TRY(regrow(m, &p, &m.ws_rows_bytes, need, s));
+        m.ws_rows = p;
+    }
+    *ws = m.ws_rows;
+    *bytes = m.ws_rows_bytes;
+    return KVHP_OK;
+}
 
 int blas_check(rocblas_status st, const char* what) {
     if (st != rocblas_status_success)
@@ -244,17 +280,7 @@ struct SuffixRows {
 int suffix_rows(Model& m, const Pages& pg, const int32_t* write_bt, int first, int rows,
                 hipStream_t s, SuffixRows& out) {
     const size_t words = 2 * (size_t)rows * pg.max_pages + 2 * (size_t)rows + 1;
-    if (m.aux_words < words) {
-        KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(aux)");
-        if (m.aux) {
-            for (auto& p : m.allocs)
-                if (p == m.aux) p = nullptr;
-            (void)hipFree(m.aux);
-            m.aux = nullptr;
-        }
-        KVHP_TRY(alloc_n(m, words, &m.aux));
-        m.aux_words = words;
-    }
+    if (m.aux_words < words) KVHP_TRY(regrow(m, &m.aux, &m.aux_words, words, s));
     out.tables = m.aux;
     out.wtables = out.tables + (size_t)rows * pg.max_pages;
     out.lens = out.wtables + (size_t)rows * pg.max_pages;
@@ -283,6 +309,9 @@ int prefill_suffix_layers(Model& m, int first, int n, const Pages& pg, const int
     KVHP_TRY(suffix_rows(m, pg, write_bt, first, S, s, sr));
     int32_t* lens = sr.lens;
     int32_t* start = sr.start;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    KVHP_TRY(rows_workspace(m, S, n, s, &ws, &ws_bytes));
     const Pages rows_pg{pg.base, pg.num_pages, sr.tables, pg.max_pages};
     KVHP_TRY(kvhp_embedding(m.tokens + first, m.embed, m.hidden, S, H, c.vocab_size, s));
     for (int l = 0; l < c.num_layers; ++l) {
@@ -294,8 +323,8 @@ int prefill_suffix_layers(Model& m, int first, int n, const Pages& pg, const int
                                       write_bt, pg.max_pages, start, 1, S, Hkv, D, pg.num_pages,
                                       s));
         const kvhp_kv_view kv = pages_view(m, rows_pg, l, 0), vv = pages_view(m, rows_pg, l, 1);
-        KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, lens, m.attn, S, Hq, Hkv, D, n, 0, nullptr,
-                                       0, s));
+        KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, lens, m.attn, S, Hq, Hkv, D, n, 0, ws,
+                                       ws_bytes, s));
         KVHP_TRY(linear(m, m.attn, L.w_o, m.hidden, S, H, Hq * D, true));
         KVHP_TRY(kvhp_rmsnorm(m.hidden, L.ffn_norm, m.norm, S, H, c.rms_eps, s));
         KVHP_TRY(linear(m, m.norm, L.w_gate_up, m.gu, S, 2 * F, H, false));
@@ -315,13 +344,17 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                 const int32_t* positions, const int32_t* seq_lens, int max_seq_len,
                 float* logits, int32_t* next, void* s, const int32_t* write_bt = nullptr) {
     // K/V appends go through write_bt when given (rows [B][max_pages] with
-    // shared pages -1), reads through pg.bt; only the fused paths take it
-    KVHP_REQUIRE(write_bt == nullptr || B <= 32, KVHP_ERR_INVALID,
-                 "decode_rows: a separate write table needs batch <= 32");
+    // shared pages -1), reads through pg.bt; only the fused paths (one row,
+    // or up to 32 on the batched projections) take it
+    KVHP_REQUIRE(write_bt == nullptr || B == 1 || (B <= 32 && m.rows_ok), KVHP_ERR_INVALID,
+                 "decode_rows: a separate write table needs the fused projections");
     const int32_t* wbt = write_bt ? write_bt : pg.bt;
     const kvhp_llama_config& c = m.c;
     const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
     const int F = c.ffn_size, NQKV = (Hq + 2 * Hkv) * D;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    KVHP_TRY(rows_workspace(m, B, max_seq_len, static_cast<hipStream_t>(s), &ws, &ws_bytes));
     KVHP_TRY(kvhp_embedding(tokens, m.embed, m.hidden, B, H, c.vocab_size, s));
     if (B == 1) {
         // one sequence: the batch-1 step's GEMV kernels (no padded MFMA columns)
@@ -334,7 +367,7 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                                                 static_cast<hipStream_t>(s)));
             const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
             KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, seq_lens, m.attn, 1, Hq, Hkv, D,
-                                           max_seq_len, 0, nullptr, 0, s));
+                                           max_seq_len, 0, ws, ws_bytes, s));
             KVHP_TRY(kvhp_gemv_residual(L.w_o, m.attn, m.hidden, m.hidden, H, Hq * D, s));
             KVHP_TRY(kvhp_rmsnorm_gemv_swiglu(L.w_gate_up, m.hidden, L.ffn_norm, c.rms_eps, m.act,
                                               F, H, s));
@@ -355,7 +388,7 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                 pg.num_pages, Hq, Hkv, D, H, B, s));
             const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
             KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, seq_lens, m.attn, B, Hq, Hkv, D,
-                                           max_seq_len, 0, nullptr, 0, s));
+                                           max_seq_len, 0, ws, ws_bytes, s));
             KVHP_TRY(kvhp_gemv_residual_rows(L.w_o, m.attn, m.hidden, m.hidden, H, Hq * D, B, s));
             KVHP_TRY(kvhp_rmsnorm_gemv_swiglu_rows(L.w_gate_up, m.hidden, L.ffn_norm, c.rms_eps,
                                                    m.act, F, H, B, s));
@@ -373,7 +406,7 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                                           m.v, s));
         const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
         KVHP_TRY(kvhp_paged_append_decode(m.q, m.k, m.v, &kv, &vv, positions, seq_lens, m.attn, B,
-                                          Hq, Hkv, D, max_seq_len, 0, nullptr, 0, s));
+                                          Hq, Hkv, D, max_seq_len, 0, ws, ws_bytes, s));
         KVHP_TRY(linear(m, m.attn, L.w_o, m.hidden, B, H, Hq * D, true));
         KVHP_TRY(kvhp_rmsnorm(m.hidden, L.ffn_norm, m.norm, B, H, c.rms_eps, s));
         KVHP_TRY(linear(m, m.norm, L.w_gate_up, m.gu, B, 2 * F, H, false));

@@ -150,6 +150,7 @@ public:
         lens_.assign(max_batch, 0);
         pos_.assign(max_batch, -1);
         pages_used_.assign(max_batch, 0);
+        cached_.assign(max_batch, 0);
         active_.assign(max_batch, false);
         free_pages_.resize(num_pages);
         for (int i = 0; i < num_pages; ++i) free_pages_[i] = num_pages - 1 - i;  // pop 0 first
@@ -214,6 +215,7 @@ public:
             e = -1;
         }
         pages_used_[slot] = 0;
+        cached_[slot] = 0;
         lens_[slot] = 0;
         pos_[slot] = -1;
         active_[slot] = false;
@@ -246,8 +248,12 @@ public:
         }
         pages_used_[dst] = n;
         lens_[dst] = n * kPage;
+        cached_[dst] = n * kPage;
         return n * kPage;
     }
+    // Leading positions of `slot` whose K/V came from share_prefix (0 after
+    // release): the most a cached-prefix prefill may take as already cached.
+    int cached_tokens(int slot) const { return cached_.at(slot); }
     // Sequences holding physical page `page` (0: free).
     int page_refs(int page) const { return refs_.at(page); }
     int seq_len(int slot) const { return lens_.at(slot); }
@@ -407,6 +413,7 @@ private:
     hipEvent_t staged_ = nullptr;
     std::vector<int32_t> tables_, lens_, pos_;
     std::vector<int> pages_used_;
+    std::vector<int> cached_;
     std::vector<bool> active_;
     std::vector<int32_t> free_pages_;
     std::vector<int> refs_;

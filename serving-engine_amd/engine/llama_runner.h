@@ -13,7 +13,9 @@
 //     sequence keep their cached K/V.  num_cached = 0 recomputes the whole
 //     prompt ("share" prefix mode, :30-33); num_cached > 0 (the tokens
 //     share_prefix() returned) forwards only the rest, which attends to the
-//     cached prefix from the pages ("full" mode).  Returns the greedy first
+//     cached prefix from the pages ("full" mode); num_cached may not exceed
+//     the tokens the slot took over (PagedKVCache::cached_tokens), since
+//     those positions are read, never written.  Returns the greedy first
 //     token.
 //   * decode_step(cache, batch, tokens): "bump, then write at num_tokens - 1"
 //     for every active slot in [0, batch) (PagedKVCache::begin_decode_step,
@@ -64,6 +66,13 @@ public:
         if (num_cached < 0 || num_cached > (int)prompt.size())
             throw std::invalid_argument("LlamaRunner::prefill: num_cached " +
                                         std::to_string(num_cached));
+        // positions below num_cached are read, not written: they must hold
+        // K/V taken over by share_prefix
+        if (num_cached > cache.cached_tokens(slot))
+            throw std::invalid_argument("LlamaRunner::prefill: num_cached " +
+                                        std::to_string(num_cached) + " exceeds the slot's " +
+                                        std::to_string(cache.cached_tokens(slot)) +
+                                        " shared-prefix tokens");
         cache.sync(stream);
         if (logits) logits->resize(config_.vocab_size);
         int32_t tok = -1;
