@@ -140,4 +140,8 @@ private:
     hipEvent_t stop_ = nullptr;
 };
 
+// The reference's name for the timer (src/common/cuda_utils.h:116-148), so
+// callers that time with it compile unchanged.
+using CudaTimer = HipTimer;
+
 }  // namespace engine

@@ -15,6 +15,15 @@
 #include "half.h"
 #include "kvhp_c.h"
 
+// Host and device qualifiers when the including file is compiled as HIP.
+#ifndef KVHP_HD
+#ifdef __HIPCC__
+#define KVHP_HD __host__ __device__
+#else
+#define KVHP_HD
+#endif
+#endif
+
 namespace engine {
 namespace hip {
 
@@ -32,17 +41,30 @@ struct KVView {
     int32_t num_pages = 0;
     int32_t reserved = 0;
 
-    // Host-side address map (the reference's get_ptr, kv_view.h:24-30, with
-    // the paged branch).  `table_host` is a host copy of the block table,
-    // needed only for a paged view.
-    const half* get_ptr(int b, int h, int s, const int32_t* table_host = nullptr) const {
-        if (!block_table)
-            return data + b * stride_b + h * stride_h + s * stride_s;
-        const int64_t page = table_host[(int64_t)b * max_pages + s / page_size];
-        return data + h * stride_h + (page * page_size + s % page_size) * stride_s;
+    // The reference's address map (kv_view.h:24-30): element (b, h, s, d)
+    // of a strided view, and of a paged view through its block table.  Both
+    // forms run in host and device code; a paged view's block_table is read
+    // where the call runs, so on the host use get_ptr_host with a host copy
+    // of a device table.
+    KVHP_HD const half* get_ptr(int b, int h, int s) const { return get_ptr(b, h, s, 0); }
+    KVHP_HD const half* get_ptr(int b, int h, int s, int d) const {
+        if (!block_table) return data + b * stride_b + h * stride_h + s * stride_s + d * stride_d;
+        return paged_ptr(block_table, b, h, s, d);
+    }
+    // Paged (or strided) address with the block table read from
+    // `table_host`, a host copy of block_table.
+    const half* get_ptr_host(int b, int h, int s, int d, const int32_t* table_host) const {
+        if (!block_table) return get_ptr(b, h, s, d);
+        return paged_ptr(table_host, b, h, s, d);
     }
 
     const kvhp_kv_view* c_view() const { return reinterpret_cast<const kvhp_kv_view*>(this); }
+
+private:
+    KVHP_HD const half* paged_ptr(const int32_t* table, int b, int h, int s, int d) const {
+        const int64_t page = table[(int64_t)b * max_pages + s / page_size];
+        return data + h * stride_h + (page * page_size + s % page_size) * stride_s + d * stride_d;
+    }
 };
 
 static_assert(sizeof(KVView) == sizeof(kvhp_kv_view), "KVView must match kvhp_kv_view");

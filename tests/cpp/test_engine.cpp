@@ -21,6 +21,7 @@
 #include <string>
 #include <vector>
 
+#include "forward_gpu.h"
 #include "hip_utils.h"
 #include "half.h"
 #include "kernels.h"
@@ -171,6 +172,36 @@ void case_host_validation() {
     EXPECT(hip::decode_workspace_bytes(3, 14, 2, 64, 600, 8) <=
                hip::decode_split_buffer_floats(3, 14, 64) * sizeof(float),
            "8-split workspace larger than the split buffer");
+}
+
+void case_kv_view_get_ptr() {
+    // reference kv_view.h:24-30: data + b*stride_b + h*stride_h + s*stride_s
+    // (+ d*stride_d), here with stride_d != 1 and a non-literal d
+    std::vector<half> buf(8192);
+    const half* base = buf.data();
+    const hip::KVView v{base, 1000, 200, 12, 3};
+    for (int b = 0; b < 3; ++b)
+        for (int h = 0; h < 2; ++h)
+            for (int s = 0; s < 5; ++s) {
+                EXPECT(v.get_ptr(b, h, s) == base + b * 1000 + h * 200 + s * 12, "(%d,%d,%d)", b, h, s);
+                for (int d = 0; d < 4; ++d)
+                    EXPECT(v.get_ptr(b, h, s, d) == base + b * 1000 + h * 200 + s * 12 + d * 3,
+                           "(%d,%d,%d,%d)", b, h, s, d);
+            }
+    // paged view: page table [2 sequences][3 pages] of a pool of 8 pages,
+    // D = 4; the table is host memory here, so get_ptr and get_ptr_host agree
+    const std::vector<int32_t> table = {5, 2, 7, 1, 0, 3};
+    const hip::KVView p = hip::paged_view(base, 8, 4, table.data(), 3);
+    for (int b = 0; b < 2; ++b)
+        for (int h = 0; h < 2; ++h)
+            for (int s = 0; s < 48; s += 5)
+                for (int d = 0; d < 4; ++d) {
+                    const half* want = base + h * (8 * 16 * 4) +
+                                       ((int64_t)table[b * 3 + s / 16] * 16 + s % 16) * 4 + d;
+                    EXPECT(p.get_ptr(b, h, s, d) == want, "paged (%d,%d,%d,%d)", b, h, s, d);
+                    EXPECT(p.get_ptr_host(b, h, s, d, table.data()) == want, "paged host");
+                }
+    EXPECT(v.get_ptr_host(1, 1, 2, 3, nullptr) == v.get_ptr(1, 1, 2, 3), "strided host form");
 }
 
 // ------------------------------------------------------------- GPU cases --
@@ -765,6 +796,125 @@ void case_llama_runner_paged() {
     EXPECT(cache.free_page_count() == cache.num_pages(), "pages leaked");
 }
 
+void case_forward_gpu_mirror() {
+    // prefill_gpu / decode_step_gpu (reference forward_gpu.h:88-113) over a
+    // KVCache against the library's own batch-1 model of the same weights:
+    // logits bit for bit, the cache bytes equal the model's pages, the
+    // lengths as the reference sets them, d_last_logits and profiling forms.
+    ModelConfig cfg;   // the reference's defaults, then a small Llama shape
+    cfg.model_type = "llama";
+    cfg.vocab_size = 1024;
+    cfg.hidden_size = 256;
+    cfg.intermediate_size = 512;
+    cfg.num_hidden_layers = 2;
+    cfg.num_attention_heads = 4;
+    cfg.num_key_value_heads = 2;
+    cfg.head_dim = 64;
+    cfg.rms_norm_eps = 1e-5f;
+    cfg.rope_theta = 10000.f;
+    cfg.tie_word_embeddings = false;
+    cfg.max_position_embeddings = 96;
+    const int M = 96, V = cfg.vocab_size;
+    const uint64_t seed = 41;
+    ModelWeightsGPU weights;
+    EXPECT(weights.init_synthetic(cfg, seed), "init_synthetic: %s", kvhp_last_error());
+    ActivationBuffersGPU buffers;
+    buffers.allocate(cfg, M);
+    KVCache kv(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, M);
+    const kvhp_llama_config c = cfg.to_c();
+    void* ref = nullptr;
+    KVHP_CHECK(kvhp_llama_create(&c, seed, M, &ref));
+
+    std::mt19937 rng(404);
+    std::vector<int64_t> prompt(37);
+    std::vector<int32_t> prompt32(prompt.size());
+    for (size_t i = 0; i < prompt.size(); ++i) prompt32[i] = (int32_t)(prompt[i] = rng() % V);
+    const std::vector<float> lg = prefill_gpu(prompt, cfg, weights, buffers, kv, nullptr);
+    std::vector<float> rl(V);
+    int32_t tok = -1;
+    KVHP_CHECK(kvhp_llama_prefill(ref, prompt32.data(), (int)prompt32.size(), rl.data(), &tok));
+    EXPECT(lg.size() == (size_t)V && std::memcmp(lg.data(), rl.data(), (size_t)V * 4) == 0,
+           "prefill logits differ");
+    EXPECT(kv.current_seq_len() == 37, "length after prefill %d", kv.current_seq_len());
+    auto same_cache = [&](const char* what) {
+        for (int l = 0; l < cfg.num_hidden_layers; ++l)
+            for (int is_v = 0; is_v < 2; ++is_v) {
+                void* pool = nullptr;
+                size_t n = 0;
+                KVHP_CHECK(kvhp_llama_tensor(ref, l, is_v ? KVHP_LLAMA_POOL_V : KVHP_LLAMA_POOL_K,
+                                             &pool, &n));
+                const size_t per = (size_t)cfg.num_key_value_heads * M * cfg.head_dim;
+                EXPECT(n == per, "%s: pool size", what);
+                std::vector<half> a(per), b(per);
+                HIP_CHECK(hipMemcpy(a.data(), kv.get_layer_ptr(l, is_v), per * 2, hipMemcpyDeviceToHost));
+                HIP_CHECK(hipMemcpy(b.data(), pool, per * 2, hipMemcpyDeviceToHost));
+                EXPECT(std::memcmp(a.data(), b.data(), per * 2) == 0, "%s: layer %d %c differs",
+                       what, l, is_v ? 'V' : 'K');
+            }
+    };
+    same_cache("after prefill");
+    int pos = 37;
+    for (int st = 0; st < 6; ++st, ++pos) {
+        const std::vector<float> dl = decode_step_gpu(tok, pos, cfg, weights, buffers, kv, nullptr);
+        int32_t next = -1;
+        KVHP_CHECK(kvhp_llama_decode_step(ref, tok, rl.data(), &next));
+        EXPECT(std::memcmp(dl.data(), rl.data(), (size_t)V * 4) == 0, "decode step %d logits", st);
+        EXPECT(kv.current_seq_len() == pos + 1, "length after step %d", st);
+        tok = next;
+    }
+    same_cache("after decode");
+    // device logits: nothing returned, the buffer holds the same values
+    DeviceBuffer<float> dlog(V);
+    const std::vector<float> none = decode_step_gpu(tok, pos, cfg, weights, buffers, kv, nullptr,
+                                                    dlog.data());
+    int32_t next = -1;
+    KVHP_CHECK(kvhp_llama_decode_step(ref, tok, rl.data(), &next));
+    EXPECT(none.empty(), "d_last_logits: host logits returned");
+    const std::vector<float> got = download(dlog);
+    EXPECT(std::memcmp(got.data(), rl.data(), (size_t)V * 4) == 0, "d_last_logits values");
+    std::vector<KernelRecord> rec;
+    (void)decode_step_gpu(next, pos + 1, cfg, weights, buffers, kv, nullptr, nullptr, &rec);
+    EXPECT(rec.size() == 1 && rec[0].ms > 0.f, "profile records");
+    kvhp_llama_destroy(ref);
+
+    // the reference's errors: a prompt longer than the buffers, and this
+    // build's: a cache whose max_seq is not whole pages, a wrong shape
+    auto throws = [](const std::function<void()>& f) {
+        try {
+            f();
+        } catch (const std::exception&) {
+            return true;
+        }
+        return false;
+    };
+    ActivationBuffersGPU small;
+    small.allocate(cfg, 16);
+    EXPECT(throws([&] { prefill_gpu(prompt, cfg, weights, small, kv, nullptr); }),
+           "prompt longer than the buffers accepted");
+    KVCache odd(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, 90);
+    EXPECT(throws([&] { prefill_gpu(prompt, cfg, weights, buffers, odd, nullptr); }),
+           "cache of 90 positions accepted");
+    KVCache shallow(1, cfg.num_key_value_heads, cfg.head_dim, M);
+    EXPECT(throws([&] { decode_step_gpu(1, 0, cfg, weights, buffers, shallow, nullptr); }),
+           "cache with the wrong layer count accepted");
+    EXPECT(throws([&] { decode_step_gpu(V, 0, cfg, weights, buffers, kv, nullptr); }),
+           "token id past the vocabulary accepted");
+
+    // tied embeddings: the LM head is the embedding
+    ModelConfig tied = cfg;
+    tied.tie_word_embeddings = true;
+    ModelWeightsGPU tw;
+    EXPECT(tw.init_synthetic(tied, seed, 32), "tied init");
+    void *e = nullptr, *h = nullptr;
+    size_t ne = 0, nh = 0;
+    KVHP_CHECK(kvhp_llama_tensor(tw.handle(), -1, KVHP_LLAMA_EMBED, &e, &ne));
+    KVHP_CHECK(kvhp_llama_tensor(tw.handle(), -1, KVHP_LLAMA_LM_HEAD, &h, &nh));
+    std::vector<half> he(ne), hh(nh);
+    HIP_CHECK(hipMemcpy(he.data(), e, ne * 2, hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(hh.data(), h, nh * 2, hipMemcpyDeviceToHost));
+    EXPECT(ne == nh && std::memcmp(he.data(), hh.data(), ne * 2) == 0, "LM head not tied");
+}
+
 struct Case {
     const char* name;
     bool gpu;
@@ -783,6 +933,7 @@ int main(int argc, char** argv) {
     const Case cases[] = {
         {"half_conversion", false, case_half_conversion},
         {"host_validation", false, case_host_validation},
+        {"kv_view_get_ptr", false, case_kv_view_get_ptr},
         {"kv_cache_layout", true, case_kv_cache_layout},
         {"append_kv_cache", true, case_append_kv_cache},
         {"decode_gqa", true, case_decode_gqa},
@@ -794,6 +945,7 @@ int main(int argc, char** argv) {
         {"paged_cache_rejects", true, case_paged_cache_rejects},
         {"paged_prefix_sharing", true, case_paged_prefix_sharing},
         {"llama_runner_paged", true, case_llama_runner_paged},
+        {"forward_gpu_mirror", true, case_forward_gpu_mirror},
     };
     for (const Case& c : cases) {
         if (c.gpu && !gpu) continue;
