@@ -89,8 +89,31 @@ void kvo_f16_to_f32_array(const uint16_t* src, float* dst, int64_t n) {
 static void attend_row(const float* q_vec, const float* k_base,
                        const float* v_base, int64_t k_stride, int64_t nkeys,
                        int64_t D, float scale, float* scores, float* out_vec) {
+    /* Four keys' dots (and below four output dims) are carried side by side
+     * as independent chains; every element keeps its own operation order. */
     float max_score = -1e30f;
-    for (int64_t j = 0; j < nkeys; ++j) {
+    int64_t j = 0;
+    for (; j + 4 <= nkeys; j += 4) {
+        const float* k0 = k_base + j * k_stride;
+        const float* k1 = k0 + k_stride;
+        const float* k2 = k1 + k_stride;
+        const float* k3 = k2 + k_stride;
+        double d0 = 0.0, d1 = 0.0, d2 = 0.0, d3 = 0.0;
+        for (int64_t d = 0; d < D; ++d) {
+            const double qd = (double)q_vec[d];
+            d0 += qd * (double)k0[d];
+            d1 += qd * (double)k1[d];
+            d2 += qd * (double)k2[d];
+            d3 += qd * (double)k3[d];
+        }
+        const double dots[4] = {d0, d1, d2, d3};
+        for (int u = 0; u < 4; ++u) {
+            float score = (float)dots[u] * scale;
+            scores[j + u] = score;
+            if (score > max_score) max_score = score;
+        }
+    }
+    for (; j < nkeys; ++j) {
         const float* k_vec = k_base + j * k_stride;
         double dot = 0.0;
         for (int64_t d = 0; d < D; ++d) dot += (double)q_vec[d] * (double)k_vec[d];
@@ -99,16 +122,32 @@ static void attend_row(const float* q_vec, const float* k_base,
         if (score > max_score) max_score = score;
     }
     double sum_exp = 0.0;
-    for (int64_t j = 0; j < nkeys; ++j) {
+    for (j = 0; j < nkeys; ++j) {
         float e = expf(scores[j] - max_score);
         scores[j] = e;
         sum_exp += (double)e;
     }
     float inv_sum = (float)(1.0 / sum_exp);
-    for (int64_t j = 0; j < nkeys; ++j) scores[j] *= inv_sum;
-    for (int64_t d = 0; d < D; ++d) {
+    for (j = 0; j < nkeys; ++j) scores[j] *= inv_sum;
+    int64_t d = 0;
+    for (; d + 4 <= D; d += 4) {
+        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+        for (j = 0; j < nkeys; ++j) {
+            const double p = (double)scores[j];
+            const float* vr = v_base + j * k_stride + d;
+            a0 += p * (double)vr[0];
+            a1 += p * (double)vr[1];
+            a2 += p * (double)vr[2];
+            a3 += p * (double)vr[3];
+        }
+        out_vec[d] = (float)a0;
+        out_vec[d + 1] = (float)a1;
+        out_vec[d + 2] = (float)a2;
+        out_vec[d + 3] = (float)a3;
+    }
+    for (; d < D; ++d) {
         double acc = 0.0;
-        for (int64_t j = 0; j < nkeys; ++j)
+        for (j = 0; j < nkeys; ++j)
             acc += (double)scores[j] * (double)v_base[j * k_stride + d];
         out_vec[d] = (float)acc;
     }
@@ -363,11 +402,11 @@ void kvo_rmsnorm(const float* x, const float* w, float* out, int64_t rows,
 }
 
 /* C[M][N] = A[M][K] * B[N][K]^T, reference matmul_transB_blocked
- * (ops.cpp:76-114): 64-wide K blocks, each block's dot in double, added to
- * the float output in block order. */
-void kvo_matmul_transB(const float* A, const float* B, float* C, int64_t M,
-                       int64_t K, int64_t N, int nthreads) {
-    if (nthreads < 1) nthreads = 1;
+ * (ops.cpp:76-114): 64-wide K blocks, each block's dot in double (products
+ * of the floats widened to double, added in k order), converted to float and
+ * added to the float output in block order. */
+static void matmul_scalar(const float* A, const float* B, float* C, int64_t M,
+                          int64_t K, int64_t N, int nthreads) {
 #pragma omp parallel for num_threads(nthreads) schedule(static) if (nthreads > 1)
     for (int64_t n = 0; n < N; ++n) {
         const float* brow = B + n * K;
@@ -383,6 +422,121 @@ void kvo_matmul_transB(const float* A, const float* B, float* C, int64_t M,
             C[m * N + n] = c;
         }
     }
+}
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+
+/* The same arithmetic, 4 rows x 8 columns at a time in AVX2 registers: lane j
+ * of a vector is one output element, so every element still sees exactly the
+ * scalar sequence (a separate IEEE double multiply and add per k in k order,
+ * no FMA: the target enables AVX2 only; round-to-nearest float conversion
+ * and float add per 64-block).  A rows of the tile beyond M repeat row M-1
+ * and are not stored.  ad: A rows [mb][K] already widened to double; bp: the
+ * panel's columns [K][8] widened, zero past N. */
+__attribute__((target("avx2")))
+static void mm_tile_rows_avx2(const double* ad, int64_t mb, const double* bp, int64_t K,
+                              float* C, int64_t ldc, int64_t nw) {
+    for (int64_t m0 = 0; m0 < mb; m0 += 4) {
+        const double* r0 = ad + m0 * K;
+        const double* r1 = ad + (m0 + 1 < mb ? m0 + 1 : mb - 1) * K;
+        const double* r2 = ad + (m0 + 2 < mb ? m0 + 2 : mb - 1) * K;
+        const double* r3 = ad + (m0 + 3 < mb ? m0 + 3 : mb - 1) * K;
+        __m128 c[4][2];
+        for (int i = 0; i < 4; ++i) c[i][0] = c[i][1] = _mm_setzero_ps();
+        for (int64_t k0 = 0; k0 < K; k0 += 64) {
+            const int64_t k1 = k0 + 64 < K ? k0 + 64 : K;
+            __m256d s00 = _mm256_setzero_pd(), s01 = _mm256_setzero_pd();
+            __m256d s10 = _mm256_setzero_pd(), s11 = _mm256_setzero_pd();
+            __m256d s20 = _mm256_setzero_pd(), s21 = _mm256_setzero_pd();
+            __m256d s30 = _mm256_setzero_pd(), s31 = _mm256_setzero_pd();
+            for (int64_t k = k0; k < k1; ++k) {
+                const __m256d b0 = _mm256_load_pd(bp + k * 8);
+                const __m256d b1 = _mm256_load_pd(bp + k * 8 + 4);
+                __m256d a = _mm256_broadcast_sd(r0 + k);
+                s00 = _mm256_add_pd(s00, _mm256_mul_pd(a, b0));
+                s01 = _mm256_add_pd(s01, _mm256_mul_pd(a, b1));
+                a = _mm256_broadcast_sd(r1 + k);
+                s10 = _mm256_add_pd(s10, _mm256_mul_pd(a, b0));
+                s11 = _mm256_add_pd(s11, _mm256_mul_pd(a, b1));
+                a = _mm256_broadcast_sd(r2 + k);
+                s20 = _mm256_add_pd(s20, _mm256_mul_pd(a, b0));
+                s21 = _mm256_add_pd(s21, _mm256_mul_pd(a, b1));
+                a = _mm256_broadcast_sd(r3 + k);
+                s30 = _mm256_add_pd(s30, _mm256_mul_pd(a, b0));
+                s31 = _mm256_add_pd(s31, _mm256_mul_pd(a, b1));
+            }
+            c[0][0] = _mm_add_ps(c[0][0], _mm256_cvtpd_ps(s00));
+            c[0][1] = _mm_add_ps(c[0][1], _mm256_cvtpd_ps(s01));
+            c[1][0] = _mm_add_ps(c[1][0], _mm256_cvtpd_ps(s10));
+            c[1][1] = _mm_add_ps(c[1][1], _mm256_cvtpd_ps(s11));
+            c[2][0] = _mm_add_ps(c[2][0], _mm256_cvtpd_ps(s20));
+            c[2][1] = _mm_add_ps(c[2][1], _mm256_cvtpd_ps(s21));
+            c[3][0] = _mm_add_ps(c[3][0], _mm256_cvtpd_ps(s30));
+            c[3][1] = _mm_add_ps(c[3][1], _mm256_cvtpd_ps(s31));
+        }
+        for (int i = 0; i < 4 && m0 + i < mb; ++i) {
+            float row[8];
+            _mm_storeu_ps(row, c[i][0]);
+            _mm_storeu_ps(row + 4, c[i][1]);
+            for (int64_t j = 0; j < nw; ++j) C[(m0 + i) * ldc + j] = row[j];
+        }
+    }
+}
+
+/* Rows in blocks of 256 (widened once, shared by the threads), columns in
+ * panels of 8 (one per task, widened into the task's buffer). */
+static int matmul_avx2(const float* A, const float* B, float* C, int64_t M, int64_t K,
+                       int64_t N, int nthreads) {
+    const int64_t MB = 256;
+    double* ad = (double*)aligned_alloc(64, sizeof(double) * (size_t)(MB * K + 8));
+    if (!ad) return -1;
+    const int64_t panels = (N + 7) / 8;
+    int failed = 0;
+    for (int64_t m0 = 0; m0 < M && !failed; m0 += MB) {
+        const int64_t mb = M - m0 < MB ? M - m0 : MB;
+#pragma omp parallel for num_threads(nthreads) schedule(static) if (nthreads > 1)
+        for (int64_t i = 0; i < mb * K; ++i) ad[i] = (double)A[m0 * K + i];
+#pragma omp parallel num_threads(nthreads) if (nthreads > 1)
+        {
+            double* bp = (double*)aligned_alloc(64, sizeof(double) * (size_t)(K * 8 + 8));
+            if (!bp) {
+#pragma omp atomic write
+                failed = 1;
+            }
+#pragma omp for schedule(dynamic, 4)
+            for (int64_t p = 0; p < panels; ++p) {
+                if (!bp) continue;
+                const int64_t n0 = p * 8;
+                const int64_t nw = N - n0 < 8 ? N - n0 : 8;
+                for (int64_t j = 0; j < 8; ++j) {
+                    const float* brow = B + (n0 + (j < nw ? j : 0)) * K;
+                    for (int64_t k = 0; k < K; ++k) bp[k * 8 + j] = j < nw ? (double)brow[k] : 0.0;
+                }
+                mm_tile_rows_avx2(ad, mb, bp, K, C + m0 * N + n0, N, nw);
+            }
+            free(bp);
+        }
+    }
+    free(ad);
+    return failed ? -1 : 0;
+}
+#endif
+
+void kvo_matmul_transB(const float* A, const float* B, float* C, int64_t M,
+                       int64_t K, int64_t N, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+#if defined(__x86_64__)
+    if (M >= 4 && __builtin_cpu_supports("avx2") && matmul_avx2(A, B, C, M, K, N, nthreads) == 0)
+        return;
+#endif
+    matmul_scalar(A, B, C, M, K, N, nthreads);
+}
+
+/* The scalar form alone (the vector form is checked against it). */
+void kvo_matmul_transB_scalar(const float* A, const float* B, float* C, int64_t M,
+                              int64_t K, int64_t N, int nthreads) {
+    matmul_scalar(A, B, C, M, K, N, nthreads < 1 ? 1 : nthreads);
 }
 
 /* Half-split RoPE, reference ops.cpp:165-221: inv_freq in float via powf,

@@ -23,7 +23,8 @@
  *   kvo_paged_*          identity block table == contiguous layout,
  *                        random permutations, drop rules
  *   kvo_rmsnorm/rope/    bit-exact vs oracle/_ref and the reference KATs
- *   swiglu/matmul        (tests/test_cpu_ops.cpp:12-110)
+ *   swiglu/matmul        (tests/test_cpu_ops.cpp:12-110); the vectorised
+ *                        matmul also bit for bit vs its scalar form
  *   kvo_f32_to_f16       against numpy float16 (IEEE RNE) on all boundaries
  */
 #ifndef KVHP_ORACLE_H
@@ -106,7 +107,12 @@ void kvo_paged_gather(const uint16_t* pool_k, const uint16_t* pool_v,
 void kvo_rmsnorm(const float* x, const float* w, float* out, int64_t rows,
                  int64_t dim, float eps);                       /* :26-51  */
 void kvo_matmul_transB(const float* A, const float* B, float* C, int64_t M,
-                       int64_t K, int64_t N, int nthreads);     /* :76-114 */
+                       int64_t K, int64_t N, int nthreads);
+/* The scalar form of kvo_matmul_transB alone (kvo_matmul_transB uses AVX2
+ * registers where the CPU has them, with the same per-element arithmetic;
+ * tests check the two bit for bit). */
+void kvo_matmul_transB_scalar(const float* A, const float* B, float* C, int64_t M,
+                              int64_t K, int64_t N, int nthreads);     /* :76-114 */
 void kvo_apply_rope(float* q, float* k, int64_t S, int64_t Hq, int64_t Hkv,
                     int64_t D, int64_t start_pos, float theta); /* :165-221 */
 void kvo_swiglu(const float* gate, const float* up, float* out,

@@ -35,9 +35,11 @@ class LlamaOracle:
     def _mm(self, a, w):
         return oracle.matmul_transB(a, w, nthreads=self.nt)
 
-    def forward(self, tokens):
+    def forward(self, tokens, logit_rows=None):
         """Run the new token ids at positions pos.. ; returns the fp32 logits
-        of the last one."""
+        of the last one, or [len(logit_rows)][V] for those rows of this call
+        (teacher forcing: one causal pass over a prompt and the tokens a model
+        generated gives every generated position's logits)."""
         c, w = self.c, self.w
         hq, hkv, d, f = c.num_q_heads, c.num_kv_heads, c.head_dim, c.ffn_size
         ids = np.asarray(tokens, np.int64)
@@ -73,8 +75,11 @@ class LlamaOracle:
             act = oracle.swiglu(np.ascontiguousarray(gu[:, :f]), np.ascontiguousarray(gu[:, f:]))
             h = h + self._mm(act, lw["w_down"])
         self.pos += s
-        last = oracle.rmsnorm(h[-1:], w["final_norm"], c.rms_eps)
-        return self._mm(last, w["lm_head"])[0]
+        if logit_rows is None:
+            last = oracle.rmsnorm(h[-1:], w["final_norm"], c.rms_eps)
+            return self._mm(last, w["lm_head"])[0]
+        rows = oracle.rmsnorm(h[np.asarray(logit_rows, np.int64)], w["final_norm"], c.rms_eps)
+        return self._mm(rows, w["lm_head"])
 
 
 def top2_margin(logits):

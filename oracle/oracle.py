@@ -50,6 +50,7 @@ _ORACLE_SIGS = {
                                 _i64, _u16p, _u16p]),
     "kvo_rmsnorm": (None, [_f32p, _f32p, _f32p, _i64, _i64, _flt]),
     "kvo_matmul_transB": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _int]),
+    "kvo_matmul_transB_scalar": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _int]),
     "kvo_apply_rope": (None, [_f32p, _f32p, _i64, _i64, _i64, _i64, _i64, _flt]),
     "kvo_swiglu": (None, [_f32p, _f32p, _f32p, _i64]),
 }
@@ -214,7 +215,7 @@ def rmsnorm(x, w, eps, use_ref=False):
     return out
 
 
-def matmul_transB(a, b, nthreads=1, use_ref=False):
+def matmul_transB(a, b, nthreads=1, use_ref=False, scalar=False):
     a = _c(a, np.float32)
     b = _c(b, np.float32)
     m, k = a.shape
@@ -222,6 +223,8 @@ def matmul_transB(a, b, nthreads=1, use_ref=False):
     out = np.empty((m, n), np.float32)
     if use_ref:
         ref().ref_matmul_transB_blocked(a, b, out, m, k, n)
+    elif scalar:
+        lib().kvo_matmul_transB_scalar(a, b, out, m, k, n, nthreads)
     else:
         lib().kvo_matmul_transB(a, b, out, m, k, n, nthreads)
     return out

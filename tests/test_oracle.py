@@ -99,6 +99,24 @@ def test_supporting_ops_golden_fixtures():
     assert np.array_equal(oracle.swiglu(g["swiglu_gate"], g["swiglu_up"]), g["swiglu_out"])
 
 
+@pytest.mark.parametrize("m,k,n", [(4, 64, 8), (5, 130, 13), (9, 2048, 33), (256, 100, 7),
+                                   (257, 700, 17), (300, 2048, 2560), (37, 5632, 24)])
+def test_matmul_vector_form_bit_exact(m, k, n):
+    """The AVX2 form of the blocked matmul (4 x 8 tiles, rows in blocks of
+    256) equals the scalar restatement of ops.cpp:76-114 bit for bit at tile,
+    block and 64-wide K-block remainders, and the reference build where it is
+    present."""
+    rng = np.random.default_rng(m * 31 + k + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k)).astype(np.float32)
+    vec = oracle.matmul_transB(a, b, nthreads=4)
+    sca = oracle.matmul_transB(a, b, nthreads=4, scalar=True)
+    assert np.array_equal(vec.view(np.uint32), sca.view(np.uint32))
+    if oracle.ref_available() and m * k * n < 5e7:
+        ref = oracle.matmul_transB(a, b, use_ref=True)
+        assert np.array_equal(vec.view(np.uint32), ref.view(np.uint32))
+
+
 def test_causal_kat_reference():
     """tests/test_cpu_ops.cpp:112-136: q=k=0.5, v[0]=1, v[1]=2 -> row 0 = v[0];
     row 1 sees two equal scores -> (1+2)/2."""
