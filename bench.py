@@ -8,25 +8,31 @@ Headline workload (the path's batched serving step):
   query per sequence over L_b + 1 keys, as one kvhp_paged_append_decode call
   (the split covering L_b writes the row and attends it from registers).
   Lengths are held fixed from step to step (each step rewrites the same
-  slot), so every timed step does identical work.
+  slot), so every timed step does identical work.  The timed steps rotate
+  over --pools (default 4) separately allocated copies of the inputs, so no
+  step finds the previous step's 504 MB in the 256 MB MALL.
 
 value = algorithmic bytes of the step (decode: K+V of every cached token once,
 q read, out write, block-table and length reads; append: new K/V read + write)
 divided by the measured step time (host clock over the timed steps).
 roofline = that call (split kernel + merge kernel), timed by one HIP event
-pair on its stream around the timed region.
+pair on its stream around the timed region; also against the device's
+measured streaming-read ceiling (kvhp_stream_read over 2 GiB, flushed), and
+beside it the same steps on one pool back to back and single flushed steps
+(median, min, max).
 cpu_baseline = the oracle's restatement of the reference CPU attention
 arithmetic (oracle/kvhp_oracle.c) on the same inputs, on the host cores.
 
 Also reported under "extra" (each measured with L2+MALL flushed by a 512 MB
-write and a 1 GiB read before every rep unless labelled warm): config 1
-(decode at ctx 512),
-config 2 (ctx 4K/16K/64K x splits 1/4/16/64), config 4 (causal prefill
+write and a 1 GiB read before every rep unless labelled warm; median, min and
+max): config 1 (decode at ctx 512), config 2 (ctx 4K/16K/64K x splits
+1/4/16/64, also against the streaming-read ceiling), config 4 (causal prefill
 S=512/2048/8192, TFLOP/s vs fp16 MFMA peak), config 5 (Llama-style 1.1B:
 2048-id prefill, then 128 greedy decode steps, tok/s and the HBM bytes of a
 step against 8 TB/s; also top-level as config5_decode_tok_s), and the KV
 movement kernels alone (paged gather of the config-3 pool, 2048-token
-appends).
+appends).  The line carries the library's build id (source hash) and whether
+it matches the sources in the tree.
 """
 import argparse
 import json
@@ -54,6 +60,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--splits", type=int, default=0, help="decode split count (0 = auto)")
+    ap.add_argument("--pools", type=int, default=4,
+                    help="separately allocated config-3 input copies the timed steps rotate "
+                         "over (504 MB each)")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 2 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5,kv")
@@ -83,8 +92,9 @@ class Flusher:
 
 
 def time_op(torch, fn, reps, flush=None):
-    """Median and mean device time (us) of fn over reps, HIP events on the
-    current stream, optional flush before each rep (outside the events)."""
+    """Device time (us) of fn over reps: (median, mean, min, max), HIP events
+    on the current stream, optional flush before each rep (outside the
+    events)."""
     stream = torch.cuda.current_stream()
     times = []
     for _ in range(reps):
@@ -97,7 +107,37 @@ def time_op(torch, fn, reps, flush=None):
         e.record(stream)
         e.synchronize()
         times.append(s.elapsed_time(e) * 1e3)
-    return float(np.median(times)), float(np.mean(times))
+    return (float(np.median(times)), float(np.mean(times)), float(np.min(times)),
+            float(np.max(times)))
+
+
+def spread(t, nbytes=None):
+    """{median, min, max} of a time_op result in us (and GB/s when nbytes)."""
+    d = {"us": round(t[0], 2), "us_min": round(t[2], 2), "us_max": round(t[3], 2)}
+    if nbytes:
+        d["GB/s"] = round(nbytes / t[0] / 1e3, 1)
+    return d
+
+
+def run_stream_read(torch, kvhp, gib=2, reps=25):
+    """The device's achievable streaming-read bandwidth (kvhp_stream_read:
+    16-byte non-temporal loads over `gib` GiB, far beyond the 256 MB MALL),
+    flushed before each rep, 5 warm-up and `reps` timed reps; the ceiling the
+    decode numbers are also reported against (as the reference calibrates
+    its decode roofline, docs/GATES.md:21)."""
+    buf = torch.ones((gib << 30) // 4, dtype=torch.float32, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    fl = Flusher(torch)
+    for _ in range(5):
+        kvhp.stream_read(buf, sink)
+    t = time_op(torch, lambda: kvhp.stream_read(buf, sink), reps, fl)
+    nbytes = buf.numel() * 4
+    del buf, fl
+    torch.cuda.empty_cache()
+    return {"GBps": round(nbytes / t[0] / 1e3, 1), "GBps_best": round(nbytes / t[2] / 1e3, 1),
+            "GBps_worst": round(nbytes / t[3] / 1e3, 1), "bytes": nbytes, "reps": reps,
+            "pct_of_spec": round(nbytes / t[0] / 1e3 / HBM_PEAK_GBS * 100, 1),
+            "kernel": "stream_read_kernel (kvhp_stream_read), flushed"}
 
 
 # ---------------------------------------------------------------- config 3 --
@@ -113,7 +153,9 @@ def append_bytes(b, hkv, d):
     return b * hkv * d * 2 * 2 * 2 + b * 4 * 2
 
 
-def build_config3(torch, kvhp, seed=3):
+def build_config3(torch, kvhp, seed=3, value_seed=None):
+    """Config-3 inputs: lengths and page tables from numpy seed `seed`, K/V
+    pool, new rows and q from torch seed `value_seed` (default `seed`)."""
     b, hq, hkv, d = 32, 32, 8, 128
     rng = np.random.default_rng(seed)
     lens = rng.integers(128, 8193, size=b).astype(np.int32)  # cached tokens
@@ -127,7 +169,7 @@ def build_config3(torch, kvhp, seed=3):
         bt[i, :n] = perm[o:o + n]
         o += int(n)
     dev = torch.device("cuda")
-    g = torch.Generator(device="cuda").manual_seed(seed)
+    g = torch.Generator(device="cuda").manual_seed(seed if value_seed is None else value_seed)
     pool_k = torch.randn((hkv, P, 16, d), generator=g, device=dev).half()
     pool_v = torch.randn((hkv, P, 16, d), generator=g, device=dev).half()
     new_k = torch.randn((b, 1, hkv, d), generator=g, device=dev).half()
@@ -201,12 +243,13 @@ def cpu_baseline_config3(c, torch):
             **host_cpu_info()}
 
 
-def cpu_baseline_config5(torch, kvhp, prompt_len=16, steps=2):
+def cpu_baseline_config5(torch, kvhp, prompt_len=16, steps=6):
     """The decoder oracle (reference CPU forward restated, with a K/V cache)
     on the config-5 model's weights read back from the GPU: a seeded
-    prompt_len-id prefill, then `steps` greedy decode steps, all host threads
-    (up to 16).  Bounded sample: the decode step's cost is dominated by the
-    2.07 GB of weights, not by the short context."""
+    prompt_len-id prefill, one untimed warm-up decode step, then `steps`
+    timed greedy decode steps (median), all host threads (up to 16).
+    Bounded sample: the decode step's cost is dominated by the 2.07 GB of
+    weights, not by the short context."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from llama_oracle import LlamaOracle
     cfg = kvhp.llama_1b_config()
@@ -232,6 +275,7 @@ def cpu_baseline_config5(torch, kvhp, prompt_len=16, steps=2):
     t0 = time.perf_counter()
     logits = ref.forward(prompt)
     t_prefill = time.perf_counter() - t0
+    logits = ref.forward([int(np.argmax(logits))])     # warm-up step, untimed
     per_tok = []
     for _ in range(steps):
         t0 = time.perf_counter()
@@ -240,13 +284,23 @@ def cpu_baseline_config5(torch, kvhp, prompt_len=16, steps=2):
     s_tok = float(np.median(per_tok))
     return {"value": round(1.0 / s_tok, 3), "unit": "tok/s", "s_per_token": round(s_tok, 3),
             "cores": threads, "kind": "port",
-            "sample": f"{prompt_len}-id prefill ({t_prefill:.2f} s, reported separately) then "
-                      f"{steps} greedy decode steps, median",
+            "sample": f"{prompt_len}-id prefill ({t_prefill:.2f} s, reported separately), one "
+                      f"warm-up step, then {steps} greedy decode steps, median "
+                      f"(min {min(per_tok):.3f} s, max {max(per_tok):.3f} s)",
             "prefill_s": round(t_prefill, 3)}
 
 
 def run_config3(torch, kvhp, args):
-    c = build_config3(torch, kvhp)
+    """The headline: config-3 steps rotating over args.pools separately
+    allocated copies of the inputs (same lengths and page tables, own K/V
+    pools, rows and queries), so between two uses of one pool the other
+    copies stream (pools - 1) x 504 MB through the caches: no step can reuse
+    the previous one's data from the 256 MB MALL (the cache-cold rule of the
+    baseline's timing).  Beside it: the same steps back to back on one pool,
+    and single steps after an explicit flush."""
+    R = max(args.pools, 1)
+    insts = [build_config3(torch, kvhp, value_seed=3 + 1000 * i) for i in range(R)]
+    c = insts[0]
     b, hq, hkv, d = c["b"], c["hq"], c["hkv"], c["d"]
     L1 = c["lens"] + 1
     max_len = int(L1.max())
@@ -256,60 +310,70 @@ def run_config3(torch, kvhp, args):
     ws_bytes = kvhp.decode_workspace_bytes(b, hq, hkv, d, max_len, splits)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device="cuda")
     kvhp.decode_workspace_init(ws)
-    kview = kvhp.paged_view(c["pool_k"], c["bt"])
-    vview = kvhp.paged_view(c["pool_v"], c["bt"])
-    new_k = c["new_k"].view(b, hkv, d)
-    new_v = c["new_v"].view(b, hkv, d)
+    for ci in insts:
+        ci["kview"] = kvhp.paged_view(ci["pool_k"], ci["bt"])
+        ci["vview"] = kvhp.paged_view(ci["pool_v"], ci["bt"])
+        ci["nk"] = ci["new_k"].view(b, hkv, d)
+        ci["nv"] = ci["new_v"].view(b, hkv, d)
     stream = torch.cuda.current_stream()
 
-    def step():
+    def step_on(ci):
         # one call: append the token at position L_b, attend over L_b + 1 keys
-        kvhp.paged_append_decode(c["q"], new_k, new_v, kview, vview, c["pos"], c["lens1"],
-                                 c["out"], hq, hkv, d, max_len, splits, ws)
+        kvhp.paged_append_decode(ci["q"], ci["nk"], ci["nv"], ci["kview"], ci["vview"], ci["pos"],
+                                 ci["lens1"], ci["out"], hq, hkv, d, max_len, splits, ws)
+
+    def step():
+        step_on(c)
 
     def append():
         kvhp.paged_append_kv(c["new_k"], c["new_v"], c["pool_k"], c["pool_v"], c["bt"],
                              c["pos"], b, 1, hkv, d)
 
     def decode():
-        kvhp.decode_attention(c["q"], kview, vview, c["lens1"], c["out"], hq, hkv, d, max_len,
-                              splits, ws)
+        kvhp.decode_attention(c["q"], c["kview"], c["vview"], c["lens1"], c["out"], hq, hkv, d,
+                              max_len, splits, ws)
 
-    for _ in range(args.warmup):
-        step()
+    def timed(n, rotate):
+        """n steps back to back (pool i % R, or pool 0), one HIP event pair
+        on the call's stream around them (no per-step records, whose markers
+        would sit between the steps' kernels) and the host clock."""
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for i in range(n):
+            step_on(insts[i % R] if rotate else c)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, ev0.elapsed_time(ev1) * 1e3
+
+    for i in range(args.warmup):
+        step_on(insts[i % R])
     torch.cuda.synchronize()
     n = args.steps
-    # Timed region: n back-to-back steps, bracketed by one HIP event pair on
-    # the call's stream (no per-step event records, whose markers would sit
-    # between the steps' kernels) and by the host clock.
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for i in range(n):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    region_us = ev0.elapsed_time(ev1) * 1e3
+    wall, region_us = timed(n, True)
     # per-step spread, from a second pass with an event pair per step
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(n)]
     for i in range(n):
         ev[i][0].record(stream)
-        step()
+        step_on(insts[i % R])
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     step_us = [s.elapsed_time(e) * 1e3 for s, e in ev]
+    same_wall, same_region_us = timed(n, False)
     step_bytes = decode_bytes(L1, hq, hkv, d) + append_bytes(b, hkv, d)
     dbytes = decode_bytes(L1, hq, hkv, d)
     res = {
         "ms_per_step": wall * 1e3 / n,
         "value": step_bytes / (wall / n) / 1e9,
         "step_us_region": region_us / n,
-        "step_us_mean": float(np.mean(step_us)),
         "step_us_median": float(np.median(step_us)),
+        "step_us_min": float(np.min(step_us)),
+        "step_us_max": float(np.max(step_us)),
+        "same_pool_us_region": same_region_us / n,
+        "pools": R,
         "decode_bytes": dbytes,
         "step_bytes": step_bytes,
         "splits": splits if splits else
@@ -321,10 +385,13 @@ def run_config3(torch, kvhp, args):
     # flushed (cold L2/MALL) times: the fused step, and for comparison the
     # same step as two calls (append kernel, then decode) and decode alone
     fl = Flusher(torch)
-    res["step_us_flushed_median"] = time_op(torch, step, 10, fl)[0]
-    res["separate_us_flushed_median"] = time_op(torch, lambda: (append(), decode()), 10, fl)[0]
-    res["decode_only_us_flushed_median"] = time_op(torch, decode, 10, fl)[0]
+    res["step_flushed"] = time_op(torch, step, 10, fl)
+    res["separate_flushed"] = time_op(torch, lambda: (append(), decode()), 10, fl)
+    res["decode_only_flushed"] = time_op(torch, decode, 10, fl)
     del fl
+    for ci in insts[1:]:
+        ci.clear()
+    torch.cuda.empty_cache()
     return res
 
 
@@ -341,8 +408,9 @@ def run_kv_movement(torch, kvhp):
     ok = torch.empty((b, hkv, cap, d), dtype=torch.float16, device="cuda")
     ov = torch.empty_like(ok)
     fl = Flusher(torch)
-    g = time_op(torch, lambda: kvhp.paged_gather_kv(c["pool_k"], c["pool_v"], c["bt"], c["lens1"],
-                                                    cap, ok, ov), 10, fl)[0]
+    gt = time_op(torch, lambda: kvhp.paged_gather_kv(c["pool_k"], c["pool_v"], c["bt"],
+                                                     c["lens1"], cap, ok, ov), 10, fl)
+    g = gt[0]
     g_read = int(L1.sum()) * hkv * d * 2 * 2
     g_write = b * hkv * cap * d * 2 * 2
     del ok, ov, c
@@ -364,7 +432,8 @@ def run_kv_movement(torch, kvhp):
     return {"workload": "paged gather of the config-3 pool (32 seqs, sum L=%d) into contiguous "
                         "K/V [32][8][%d][128]; append of 2048 tokens x 8 heads x D=128" % (
                             int(L1.sum()), cap),
-            "gather_us": round(g, 2), "gather_bytes": g_read + g_write,
+            "gather_us": round(g, 2), "gather_us_min": round(gt[2], 2),
+            "gather_us_max": round(gt[3], 2), "gather_bytes": g_read + g_write,
             "gather_GBps": round((g_read + g_write) / g / 1e3, 1),
             "paged_append_2048_us": round(a_p, 2),
             "contig_append_2048_us": round(a_c, 2), "append_bytes": a_bytes,
@@ -388,15 +457,16 @@ def run_config1(torch, kvhp):
 
     for _ in range(10):
         step()
-    warm_med, _ = time_op(torch, step, 50)
+    warm = time_op(torch, step, 50)
     fl = Flusher(torch)
-    cold_med, _ = time_op(torch, step, 20, fl)
+    cold = time_op(torch, step, 20, fl)
     return {"workload": "config1: append 1 token at pos 511 + decode ctx 512, 32/8 heads, D=64",
-            "us_per_step_flushed": round(cold_med, 2), "us_per_step_warm": round(warm_med, 2),
+            "us_per_step_flushed": round(cold[0], 2), "flushed": spread(cold),
+            "us_per_step_warm": round(warm[0], 2), "warm": spread(warm),
             "bytes": decode_bytes([512], hq, hkv, d) + append_bytes(1, hkv, d)}
 
 
-def run_config2(torch, kvhp):
+def run_config2(torch, kvhp, stream_gbps=None):
     hq, hkv, d = 32, 8, 128
     fl = Flusher(torch)
     rows = []
@@ -420,10 +490,12 @@ def run_config2(torch, kvhp):
 
             for _ in range(3):
                 fn()
-            med, _ = time_op(torch, fn, 15, fl)
-            rows.append({"ctx": L, "splits": s if s else f"auto({kvhp.decode_auto_splits(1, hkv, d, L)})",
-                         "us": round(med, 2), "GB/s": round(nb / med / 1e3, 1),
-                         "pct_hbm": round(nb / med / 1e3 / HBM_PEAK_GBS * 100, 1)})
+            t = time_op(torch, fn, 15, fl)
+            row = {"ctx": L, "splits": s if s else f"auto({kvhp.decode_auto_splits(1, hkv, d, L)})",
+                   **spread(t, nb), "pct_hbm": round(nb / t[0] / 1e3 / HBM_PEAK_GBS * 100, 1)}
+            if stream_gbps:
+                row["pct_stream"] = round(nb / t[0] / 1e3 / stream_gbps * 100, 1)
+            rows.append(row)
         del kc, vc
     return {"workload": "config2: B=1, 32/8 heads, D=128, contiguous fp16 KV, flushed", "rows": rows}
 
@@ -444,10 +516,10 @@ def run_config4(torch, kvhp, sizes=(512, 2048, 8192), reps=10):
 
         for _ in range(3):
             fn()
-        med, _ = time_op(torch, fn, reps, fl)
+        t = time_op(torch, fn, reps, fl)
         flops = 2.0 * d * hq * s * (s + 1)
-        tf = flops / med / 1e6
-        rows.append({"S": s, "us": round(med, 2), "TFLOP/s": round(tf, 1),
+        tf = flops / t[0] / 1e6
+        rows.append({"S": s, **spread(t), "TFLOP/s": round(tf, 1),
                      "pct_fp16_peak": round(tf / FP16_PEAK_TFLOPS * 100, 2)})
     return {"workload": "config4: causal prefill B=1, 32/8 heads, D=128, fp16 in / fp32 acc",
             "rows": rows}
@@ -602,12 +674,15 @@ def main():
             rb = run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=args.steps)
             print(json.dumps({"profile": "batched", "config5_batched": rb}))
             return
+    log("stream-read ceiling ...")
+    sr = run_stream_read(torch, kvhp)
     log("config3 timed steps ...")
     r = run_config3(torch, kvhp, args)
     c = r.pop("c")
     dbytes = r["decode_bytes"]
     sbytes = r["step_bytes"]
     achieved = sbytes / r["step_us_region"] / 1e3
+    fl_step, fl_sep, fl_dec = r["step_flushed"], r["separate_flushed"], r["decode_only_flushed"]
     line = {
         "metric": METRIC,
         "value": round(r["value"], 2),
@@ -622,30 +697,42 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic N(0,1) fp16, seeded (torch generator 3; lengths numpy seed 3)",
+        "data": "synthetic N(0,1) fp16, seeded (torch generators 3, 1003, ...; lengths numpy "
+                "seed 3)",
+        "build_id": kvhp.build_id(),
+        "build_id_matches_sources": kvhp.build_id() == kvhp.source_build_id(),
         "config": {
             "workload": "BASELINE config 3: batched paged decode step, B=32, L~U[128,8192] "
                         "(seed 3), 32 q / 8 KV heads, D=128, 16-token pages, random-permutation "
-                        "block tables; step = paged append 1 token/seq + split-K decode",
+                        "block tables; step = paged append 1 token/seq + split-K decode; steps "
+                        f"rotate over {r['pools']} separately allocated input copies (no step "
+                        "reuses the previous step's data from the 256 MB MALL)",
             "sum_L": r["sum_L"], "splits": r["splits"], "decode_bytes": dbytes,
-            "step_bytes": r["step_bytes"]},
+            "step_bytes": r["step_bytes"], "pools": r["pools"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(dbytes),
                      "kernel": "decode_splitk_kernel<128,4,true> (append fused) + "
                                "decode_merge_kernel<128,4>: one kvhp_paged_append_decode call",
                      "avg_launch_us": round(r["step_us_region"], 2),
-                     "per_step_event_us_median": round(r["step_us_median"], 2),
-                     "flushed_launch_us": round(r["step_us_flushed_median"], 2),
-                     "flushed_GBps": round(sbytes / r["step_us_flushed_median"] / 1e3, 1),
-                     "separate_calls_flushed_us": round(r["separate_us_flushed_median"], 2),
-                     "decode_only_flushed_us": round(r["decode_only_us_flushed_median"], 2),
-                     "decode_only_flushed_GBps": round(
-                         dbytes / r["decode_only_us_flushed_median"] / 1e3, 1),
+                     "per_step_event_us": {"median": round(r["step_us_median"], 2),
+                                           "min": round(r["step_us_min"], 2),
+                                           "max": round(r["step_us_max"], 2)},
+                     "stream_read": sr,
+                     "frac_of_stream_read": round(achieved / sr["GBps"], 4),
+                     "same_pool_back_to_back_us": round(r["same_pool_us_region"], 2),
+                     "same_pool_back_to_back_GBps": round(sbytes / r["same_pool_us_region"] / 1e3, 1),
+                     "flushed": {**spread(fl_step, sbytes),
+                                 "frac": round(sbytes / fl_step[0] / 1e3 / HBM_PEAK_GBS, 4)},
+                     "separate_calls_flushed": spread(fl_sep, sbytes),
+                     "decode_only_flushed": spread(fl_dec, dbytes),
                      "note": "achieved = algorithmic bytes of the step / (HIP-event time of the "
-                             "timed region / steps), one call per step (working set 504 MB vs 256 MB "
-                             "MALL); flushed = after a 512 MB write + 1 GiB read; separate = the same step as "
-                             "kvhp_paged_append_kv + kvhp_decode_attention"},
+                             "timed region / steps), one call per step, steps rotating over the "
+                             "input copies; same_pool = the steps back to back on one copy; "
+                             "flushed = single steps after a 512 MB write + 1 GiB read (median, "
+                             "min, max of 10); separate = the step as kvhp_paged_append_kv + "
+                             "kvhp_decode_attention; stream_read = the device's streaming-read "
+                             "ceiling (kvhp_stream_read over 2 GiB, flushed)"},
     }
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -663,7 +750,7 @@ def main():
             extra["config1"] = run_config1(torch, kvhp)
         if "c2" in parts:
             log("config2 ...")
-            extra["config2"] = run_config2(torch, kvhp)
+            extra["config2"] = run_config2(torch, kvhp, sr["GBps"])
         if "c4" in parts:
             log("config4 ...")
             extra["config4"] = run_config4(torch, kvhp)

@@ -68,6 +68,21 @@ const char* kvhp_last_error(void);
 /* ABI version of this library (KVHP_ABI_VERSION). */
 int kvhp_abi_version(void);
 #define KVHP_ABI_VERSION 1
+/* Build id of this library: the first 16 hex digits of the SHA-256 of its
+ * sources (the .hip, then the .h files of its csrc directory, each set in
+ * name order, then this header),
+ * fixed when the library is linked, so a result can be tied to the sources
+ * it ran. */
+const char* kvhp_build_id(void);
+
+/* Streaming-read calibration, the reference's read-bandwidth probe
+ * (src/cuda/read_bandwidth.cu:8-118; its measured ceiling is the roofline of
+ * docs/GATES.md:21): reads `bytes` (rounded down to 16) of device memory
+ * once with 16-byte non-temporal loads and writes nothing (sink, 4 bytes of
+ * device memory, is written only if the data fold equals a fixed constant).
+ * Time it over a buffer larger than the 256 MB MALL with the caches flushed
+ * to get the device's achievable read bandwidth. */
+int kvhp_stream_read(const void* buf, size_t bytes, void* sink, void* stream);
 
 /* Replaces engine::cuda::append_kv_cache (src/runtime/kv_cache.h:80-91,
  * kernel src/runtime/kv_cache.cu:8-61).  src [num_tokens][Hkv][D] token-major

@@ -72,6 +72,8 @@ _SIGNATURES = {
     "kvhp_decode_workspace_init": (_i32, [_vp, _sz, _vp]),
     "kvhp_decode_attention": (_i32, [_vp, ctypes.POINTER(KVView), ctypes.POINTER(KVView), _vp,
                                      _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "kvhp_build_id": (ctypes.c_char_p, []),
+    "kvhp_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
     "kvhp_paged_append_decode": (_i32, [_vp, _vp, _vp, ctypes.POINTER(KVView),
                                         ctypes.POINTER(KVView), _vp, _vp, _vp, _i32, _i32, _i32,
                                         _i32, _i32, _i32, _vp, _sz, _vp]),
@@ -142,6 +144,34 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
 
 def exported_symbols() -> list:
     return list(_SIGNATURES)
+
+
+def build_id() -> str:
+    """Source hash the loaded library was linked with (kvhp_build_id)."""
+    return load().kvhp_build_id().decode()
+
+
+def source_build_id(root: str = os.path.dirname(os.path.abspath(__file__))) -> str:
+    """The same hash over the sources in this tree (Makefile ID_SRCS): the
+    library matches the tree when build_id() == source_build_id()."""
+    import glob
+    import hashlib
+    csrc = os.path.join(root, "csrc")
+    files = (sorted(glob.glob(os.path.join(csrc, "*.hip"))) +
+             sorted(glob.glob(os.path.join(csrc, "*.h"))) +
+             [os.path.join(root, "..", "include", "kvhp_c.h")])
+    h = hashlib.sha256()
+    for f in files:
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def stream_read(buf, sink, stream=None):
+    """Streaming read of the whole tensor `buf` (kvhp_stream_read); sink: a
+    device tensor of at least 4 bytes."""
+    _check(load().kvhp_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
+                                   _stream(stream)))
 
 
 def last_error() -> str:
