@@ -151,6 +151,23 @@ int kvhp_decode_attention(const void* q, const kvhp_kv_view* k_view,
                           int num_splits, void* workspace,
                           size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference: kvhp_decode_attention for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops that forbid hipMalloc).  Same arguments and results as
+ * kvhp_decode_attention with workspace = NULL, but the split partials live
+ * in a static 16 MiB device array of the library (one per GPU, held until
+ * the process ends) instead of an allocated buffer; the call allocates
+ * nothing.  A plan whose partials exceed 16 MiB is rejected with
+ * KVHP_ERR_WORKSPACE (config 3's auto plan needs 11.2 MB).  Every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU (other streams
+ * or threads) race.  Partials need no clearing: a call reads only the ones
+ * it wrote. */
+int kvhp_decode_attention_noalloc(const void* q, const kvhp_kv_view* k_view,
+                                  const kvhp_kv_view* v_view, const int32_t* seq_lens,
+                                  void* out, int batch, int num_q_heads, int num_kv_heads,
+                                  int head_dim, int max_seq_len, int num_splits,
+                                  void* stream);
+
 /* The serving step's append_kv_cache + decode_gqa_split pair
  * (src/model/forward_gpu.cu:593-640: append the new K/V row at pos, then
  * attend over pos+1 keys) in one call on paged views:

@@ -745,6 +745,30 @@ size_t workspace_bytes_for(int batch, int hq, int hkv, int d, const Plan& p) {
     return sizeof(float) * (size_t)batch * hq * p.nsplit * (d + 2);
 }
 
+// Static split-partial scratch of kvhp_decode_attention_noalloc: 16 MiB
+// per device (config 3's auto plan needs 11.2 MB), held until the process
+// ends.  Kernels get it through the address hipGetSymbolAddress returns for
+// the current device (scratch_address), never through the host-side name.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+std::mutex g_scratch_mutex;
+std::vector<void*> g_scratch;   // device address of `scratch`, per device
+
+int scratch_address(void** out) {
+    int dev = 0;
+    KVHP_HIP(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if ((int)g_scratch.size() <= dev) g_scratch.resize(dev + 1, nullptr);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        KVHP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return KVHP_OK;
+}
+
 // Library-owned per-device workspace used when the caller passes none.
 struct DeviceWorkspace {
     void* ptr = nullptr;
@@ -1040,6 +1064,32 @@ extern "C" int kvhp_decode_attention(const void* q, const kvhp_kv_view* k_view,
     return decode_attention_impl(q, k_view, v_view, seq_lens, 0, out, batch, num_q_heads,
                                  num_kv_heads, head_dim, max_seq_len, num_splits, workspace,
                                  workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvhp_decode_attention_noalloc(const void* q, const kvhp_kv_view* k_view,
+                                             const kvhp_kv_view* v_view,
+                                             const int32_t* seq_lens, void* out, int batch,
+                                             int num_q_heads, int num_kv_heads, int head_dim,
+                                             int max_seq_len, int num_splits, void* stream) {
+    clear_error();
+    KVHP_REQUIRE(seq_lens, KVHP_ERR_INVALID, "decode_attention_noalloc: null seq_lens");
+    KVHP_REQUIRE(k_view && v_view, KVHP_ERR_INVALID, "decode_attention_noalloc: null view");
+    if (batch <= 0 || max_seq_len <= 0) return KVHP_OK;
+    // the split partials of the plan this call will run, against the scratch
+    const bool paged = k_view->block_table != nullptr;
+    const size_t need = workspace_bytes_for(
+        batch, num_q_heads, num_kv_heads, head_dim,
+        plan_for(batch, num_kv_heads, max_seq_len, num_splits, paged));
+    KVHP_REQUIRE(need <= kScratchBytes, KVHP_ERR_WORKSPACE,
+                 "decode_attention_noalloc: %zu bytes of split partials needed, the static "
+                 "scratch holds %zu (use kvhp_decode_attention with a workspace)",
+                 need, kScratchBytes);
+    void* ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc) return rc;
+    return decode_attention_impl(q, k_view, v_view, seq_lens, 0, out, batch, num_q_heads,
+                                 num_kv_heads, head_dim, max_seq_len, num_splits, ws,
+                                 kScratchBytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int kvhp_paged_append_decode(const void* q, const void* k_new, const void* v_new,

@@ -74,6 +74,8 @@ _SIGNATURES = {
                                      _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
     "kvhp_build_id": (ctypes.c_char_p, []),
     "kvhp_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
+    "kvhp_decode_attention_noalloc": (_i32, [_vp, ctypes.POINTER(KVView), ctypes.POINTER(KVView),
+                                             _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "kvhp_paged_append_decode": (_i32, [_vp, _vp, _vp, ctypes.POINTER(KVView),
                                         ctypes.POINTER(KVView), _vp, _vp, _vp, _i32, _i32, _i32,
                                         _i32, _i32, _i32, _vp, _sz, _vp]),
@@ -269,6 +271,16 @@ def decode_attention(q, k_view: KVView, v_view: KVView, seq_lens, out, num_q_hea
         _ptr(q), ctypes.byref(k_view), ctypes.byref(v_view), _ptr(seq_lens), _ptr(out),
         seq_lens.shape[0], num_q_heads, num_kv_heads, head_dim, max_seq_len, num_splits,
         _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+def decode_attention_noalloc(q, k_view: KVView, v_view: KVView, seq_lens, out, num_q_heads,
+                             num_kv_heads, head_dim, max_seq_len, num_splits=0, stream=None):
+    """decode_attention with the split partials in the library's static
+    device scratch (no allocation; calls overlapping on one GPU race)."""
+    _check(load().kvhp_decode_attention_noalloc(
+        _ptr(q), ctypes.byref(k_view), ctypes.byref(v_view), _ptr(seq_lens), _ptr(out),
+        seq_lens.shape[0], num_q_heads, num_kv_heads, head_dim, max_seq_len, num_splits,
+        _stream(stream)))
 
 
 def paged_append_decode(q, k_new, v_new, k_view: KVView, v_view: KVView, positions, seq_lens,

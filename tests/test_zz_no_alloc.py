@@ -1,0 +1,93 @@
+"""kvhp_decode_attention_noalloc (split partials in the library's static
+device scratch, no allocation) through the C ABI, against
+kvhp_decode_attention on the same inputs: outputs bit for bit, on two calls
+in a row, the second smaller (the scratch keeps the first call's partials),
+and both against the oracle within the attention tolerance (max-abs 2e-3 /
+max-rel 1e-2).  A plan whose partials exceed the scratch is refused before
+any launch.
+"""
+import numpy as np
+import pytest
+
+import kvhp
+import oracle
+from gpu_util import assert_attn_close, from_gpu, make_block_tables, note, sync, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _pool_case(rng, lens, hq, hkv, d):
+    """Random fp16 pool [Hkv][P][16][D] on the GPU, seeded random page
+    tables; returns (q, k view, v view, seq_lens, oracle reference)."""
+    lens = np.asarray(lens, np.int32)
+    b = lens.size
+    bt, P = make_block_tables(rng, lens)
+    gen = torch.Generator(device="cuda").manual_seed(int(rng.integers(1 << 30)))
+    pk = torch.randn((hkv, P, 16, d), generator=gen, device="cuda").half()
+    pv = torch.randn((hkv, P, 16, d), generator=gen, device="cuda").half()
+    q = torch.randn((b, hq, d), generator=gen, device="cuda").half()
+    bt_t = to_gpu(bt)
+    views = (kvhp.paged_view(pk, bt_t), kvhp.paged_view(pv, bt_t))
+    cap = max(int(lens.max()), 1)
+    hk, hv = from_gpu(pk).astype(np.float32), from_gpu(pv).astype(np.float32)
+    kc = np.zeros((b, hkv, cap, d), np.float32)
+    vc = np.zeros_like(kc)
+    for i in range(b):
+        n = int(lens[i])
+        pages = bt[i, :(n + 15) // 16]
+        kc[i, :, :n] = hk[:, pages].reshape(hkv, -1, d)[:, :n]
+        vc[i, :, :n] = hv[:, pages].reshape(hkv, -1, d)[:, :n]
+    ref = oracle.decode_attention(from_gpu(q).astype(np.float32), kc, vc, lens, hq, hkv, d,
+                                  nthreads=16)
+    return q, views, to_gpu(lens), ref, (pk, pv, bt_t)
+
+
+def _both(q, views, lens_t, hq, hkv, d, max_len, splits):
+    b = lens_t.shape[0]
+    a = torch.full((b, hq, d), float("nan"), dtype=torch.float16, device="cuda")
+    n = torch.full_like(a, float("nan"))
+    kvhp.decode_attention(q, views[0], views[1], lens_t, a, hq, hkv, d, max_len, splits)
+    kvhp.decode_attention_noalloc(q, views[0], views[1], lens_t, n, hq, hkv, d, max_len, splits)
+    sync()
+    return from_gpu(a), from_gpu(n)
+
+
+def test_noalloc_matches_allocating_entry_point_twice():
+    rng = np.random.default_rng(77)
+    # call 1: BASELINE config 3 shape (32 sequences, lengths in [128, 8192],
+    # 32/8 heads, D=128), auto splits: the device-balanced plan, 11.2 MB of
+    # partials in the scratch
+    lens1 = rng.integers(128, 8193, size=32).astype(np.int32)
+    note(f"noalloc call 1: B=32 sum L={int(lens1.sum())}")
+    q, views, lt, ref, keep = _pool_case(rng, lens1, 32, 8, 128)
+    a, n = _both(q, views, lt, 32, 8, 128, int(lens1.max()), 0)
+    assert np.array_equal(a.view(np.uint16), n.view(np.uint16)), "call 1: outputs differ"
+    assert_attn_close(n.astype(np.float32), ref, "noalloc call 1")
+    del keep, views
+    # call 2, smaller: 4 sequences (one empty), 32/4 heads of 64, 4 explicit
+    # splits; the scratch still holds call 1's partials
+    lens2 = np.array([700, 33, 0, 2000], np.int32)
+    note(f"noalloc call 2: lens {lens2.tolist()}")
+    q, views, lt, ref, keep = _pool_case(rng, lens2, 32, 4, 64)
+    a, n = _both(q, views, lt, 32, 4, 64, int(lens2.max()), 4)
+    assert np.array_equal(a.view(np.uint16), n.view(np.uint16)), "call 2: outputs differ"
+    assert_attn_close(n.astype(np.float32), ref, "noalloc call 2")
+
+
+def test_noalloc_refuses_plans_beyond_the_scratch():
+    """256 sequences x 32 heads x 64 splits x (128 + 2) floats = 272 MB of
+    partials: refused with KVHP_ERR_WORKSPACE before any launch.  (Every
+    length is 0, so nothing would be read even if a launch happened.)"""
+    b, hq, hkv, d = 256, 32, 8, 128
+    k = torch.zeros((hkv, 16, d), dtype=torch.float16, device="cuda")
+    view = kvhp.strided_view(k, 0, 16 * d, d)
+    out = torch.zeros((b, hq, d), dtype=torch.float16, device="cuda")
+    lens = torch.zeros(b, dtype=torch.int32, device="cuda")
+    with pytest.raises(kvhp.KVHPError) as e:
+        kvhp.decode_attention_noalloc(torch.zeros((b, hq, d), dtype=torch.float16, device="cuda"),
+                                      view, view, lens, out, hq, hkv, d, 65536, 64)
+    assert e.value.code == kvhp.KVHP_ERR_WORKSPACE, e.value
+    assert "static scratch" in str(e.value)
+    sync()
