@@ -218,6 +218,19 @@ kvhp_kv_view pages_view(const Model& m, const Pages& pg, int l, int is_v) {
 
 Pages own_pages(const Model& m) { return Pages{m.pool, m.P, m.bt, m.P}; }
 
+// The model's own pages are in identity order, so its pool [Hkv][P][16][D]
+// is the contiguous cache [Hkv][16 P][D]: the batch-1 step reads it through
+// a strided view, with no block-table load ahead of the first K/V load.
+kvhp_kv_view own_view(const Model& m, int l, int is_v) {
+    kvhp_kv_view v{};
+    v.data = layer_pool(m, own_pages(m), l, is_v);
+    v.stride_b = 0;
+    v.stride_h = (int64_t)m.P * kPage * m.c.head_dim;
+    v.stride_s = m.c.head_dim;
+    v.stride_d = 1;
+    return v;
+}
+
 // rocBLAS follows `s` for the lifetime of this object, then the model's
 // stream again.
 struct BlasOn {
@@ -432,9 +445,8 @@ int decode_step_kernels(Model& m, bool embed_token) {
         KVHP_TRY(kvhp_rmsnorm_qkv_rope_append(L.w_qkv, m.x, L.attn_norm, c.rms_eps, m.state,
                                               c.rope_theta, m.q1, L.pool_k, L.pool_v, m.bt, m.P,
                                               m.P, Hq, Hkv, D, H, s));
-        const Pages pg = own_pages(m);
         const int l = static_cast<int>(&L - m.layers.data());
-        const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
+        const kvhp_kv_view kv = own_view(m, l, 0), vv = own_view(m, l, 1);
         KVHP_TRY(kvhp_decode_attention(m.q1, &kv, &vv, m.state, m.attn1, 1, Hq, Hkv, D, m.max_ctx,
                                        0, m.ws, m.ws_bytes, s));
         KVHP_TRY(kvhp_gemv_residual(L.w_o, m.attn1, m.x, m.x, H, Hq * D, s));
