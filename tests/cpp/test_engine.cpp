@@ -776,6 +776,23 @@ void case_llama_runner_paged() {
         threw = true;
     }
     EXPECT(threw, "prefill with a length other than the slot's accepted");
+    // num_cached beyond the tokens the slot took over by share_prefix: those
+    // positions would be read from pages nothing wrote
+    EXPECT(cache.cached_tokens(2) == 32 && cache.cached_tokens(1) == 0, "cached token counts");
+    threw = false;
+    try {
+        runner.prefill(cache, 1, prompts[1], nullptr, nullptr, 16);   // slot 1 shares nothing
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    EXPECT(threw, "num_cached beyond the shared prefix accepted");
+    threw = false;
+    try {
+        runner.prefill(cache, 2, prompts[2], nullptr, nullptr, 33);   // 32 shared tokens
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    EXPECT(threw, "num_cached 33 over a 32-token shared prefix accepted");
     for (int st = 0; st < 4; ++st) {
         std::vector<float> lg;
         const std::vector<int32_t> next = runner.decode_step(cache, 4, last, &lg);
