@@ -515,26 +515,19 @@ def run_config2(torch, kvhp, stream_gbps=None):
     return {"workload": "config2: B=1, 32/8 heads, D=128, contiguous fp16 KV, flushed", "rows": rows}
 
 
-def run_config4(torch, kvhp, sizes=(512, 2048, 8192), reps=10):
+def run_config4(torch, kvhp, sizes=(512, 2048, 8192), reps=10, attention_only=True):
+    """causal prefill that writes K/V into 16-token pages as
+    it runs (kvhp_flash_prefill_paged, a seeded random page permutation); the
+    same prefill without the page writes is reported beside it."""
     hq, hkv, d = 32, 8, 128
     rows = []
     fl = Flusher(torch)
-    for s in sizes:
-        g = torch.Generator(device="cuda").manual_seed(s)
-        q = torch.randn((s, hq, d), generator=g, device="cuda").half()
-        k = torch.randn((s, hkv, d), generator=g, device="cuda").half()
-        v = torch.randn((s, hkv, d), generator=g, device="cuda").half()
-        out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
 
-        def fn():
-            kvhp.flash_prefill(q, k, v, out, s, hq, hkv, d, 1)
-
-        for _ in range(3):
-            fn()
+    def back_to_back(fn):
         # MFMA-bound: timed back to back (the inputs come straight from the
         # projection GEMMs in a serving step, cache-warm), 5 runs of `reps`
-        # calls under one event pair; the flushed single call beside it
-        stream = torch.cuda.current_stream()
+        # calls under one event pair
         warm = []
         for _ in range(5):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -544,17 +537,48 @@ def run_config4(torch, kvhp, sizes=(512, 2048, 8192), reps=10):
             e1.record(stream)
             e1.synchronize()
             warm.append(e0.elapsed_time(e1) * 1e3 / reps)
-        t = (float(np.median(warm)), float(np.mean(warm)), float(np.min(warm)), float(np.max(warm)))
-        tfl = time_op(torch, fn, reps, fl)
+        return (float(np.median(warm)), float(np.mean(warm)), float(np.min(warm)), float(np.max(warm)))
+
+    for s in sizes:
+        g = torch.Generator(device="cuda").manual_seed(s)
+        q = torch.randn((s, hq, d), generator=g, device="cuda").half()
+        k = torch.randn((s, hkv, d), generator=g, device="cuda").half()
+        v = torch.randn((s, hkv, d), generator=g, device="cuda").half()
+        out = torch.empty_like(q)
+        npages = (s + 15) // 16
+        pool_k = torch.zeros((hkv, npages, 16, d), dtype=torch.float16, device="cuda")
+        pool_v = torch.zeros_like(pool_k)
+        perm = np.random.default_rng(s).permutation(npages).astype(np.int32)
+        bt = torch.from_numpy(perm[None, :].copy()).cuda()
+
+        def paged():
+            kvhp.flash_prefill_paged(q, k, v, out, s, hq, hkv, d, 1, pool_k, pool_v, bt)
+
+        def plain():
+            kvhp.flash_prefill(q, k, v, out, s, hq, hkv, d, 1)
+
+        for _ in range(3):
+            paged()
         flops = 2.0 * d * hq * s * (s + 1)
-        tf = flops / t[0] / 1e6
-        rows.append({"S": s, **spread(t), "TFLOP/s": round(tf, 1),
-                     "pct_fp16_peak": round(tf / FP16_PEAK_TFLOPS * 100, 2),
-                     "flushed": {**spread(tfl),
-                                 "pct_fp16_peak": round(flops / tfl[0] / 1e6 / FP16_PEAK_TFLOPS * 100,
-                                                        2)}})
-    return {"workload": "config4: causal prefill B=1, 32/8 heads, D=128, fp16 in / fp32 acc; "
-                        "back-to-back calls (median of 5 runs), flushed single calls beside",
+        pct = lambda us: round(flops / us / 1e6 / FP16_PEAK_TFLOPS * 100, 2)
+        t = back_to_back(paged)
+        tfl = time_op(torch, paged, reps, fl)
+        row = {"S": s, **spread(t), "TFLOP/s": round(flops / t[0] / 1e6, 1),
+               "pct_fp16_peak": pct(t[0]),
+               "flushed": {**spread(tfl), "pct_fp16_peak": pct(tfl[0])}}
+        if attention_only:
+            for _ in range(3):
+                plain()
+            ta = back_to_back(plain)
+            tafl = time_op(torch, plain, reps, fl)
+            row["attention_only"] = {**spread(ta), "pct_fp16_peak": pct(ta[0]),
+                                     "flushed": {**spread(tafl), "pct_fp16_peak": pct(tafl[0])}}
+        rows.append(row)
+    return {"workload": "config4: causal prefill B=1, 32/8 heads, D=128, fp16 in / fp32 acc, "
+                        "K/V written into 16-token pages (seeded random page order) as the "
+                        "prefill runs (kvhp_flash_prefill_paged); back-to-back calls (median "
+                        "of 5 runs), flushed single calls beside; attention_only = the same "
+                        "prefill without the page writes",
             "rows": rows}
 
 
@@ -696,7 +720,7 @@ def main():
         del src, dst
         if args.profile == "prefill":
             # S=2048 runs the key-split kernel, S=8192 the ping-pong one
-            r4 = run_config4(torch, kvhp, sizes=(2048, 8192), reps=args.steps)
+            r4 = run_config4(torch, kvhp, sizes=(2048, 8192), reps=args.steps, attention_only=False)
             print(json.dumps({"profile": "prefill", "config4": r4}))
             return
         if args.profile == "c5":

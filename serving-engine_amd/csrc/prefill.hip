@@ -562,6 +562,36 @@ prefill_mfma_kernel(const PrefillArgs a) {
         }
         wait_vmcnt<0>();  // drain the ring's trailing re-loads
 
+        // ---- pages: this query block's own K/V rows, once per KV head.  Rows
+        //      of the pass's last tile come from its ring stage (still intact:
+        //      the trailing re-loads go to the other stages), earlier rows
+        //      (blocks longer than a tile) from memory.
+        if (a.pool_k) {
+            const int lt0 = last_tile * kBN;
+            const f16* Ks = ring + (last_tile % NSTAGE) * 2 * TB;
+            const f16* Vs = Ks + TB;
+            for (int idx = tid; idx < BM * CPR; idx += NTH) {
+                const int key = q0 + idx / CPR;
+                const int ch = idx % CPR;
+                if (key >= S || key / kPage >= a.max_pages) continue;
+                const int pid = a.bt[(int64_t)b * a.max_pages + key / kPage];
+                if (pid < 0 || pid >= a.num_pages) continue;
+                const int64_t dst =
+                    (((int64_t)kvh * a.num_pages + pid) * kPage + key % kPage) * D + 8 * ch;
+                half8 kk, vv;
+                if (key >= lt0) {
+                    const int r = key - lt0;
+                    kk = *reinterpret_cast<const half8*>(&Ks[r * D + 8 * (ch ^ (r & KSW))]);
+                    vv = *reinterpret_cast<const half8*>(&Vs[r * D + 8 * (ch ^ vswz(r))]);
+                } else {
+                    kk = load_half8(kb + (int64_t)key * kvrs + 8 * ch);
+                    vv = load_half8(vb + (int64_t)key * kvrs + 8 * ch);
+                }
+                store_half8(a.pool_k + dst, kk);
+                store_half8(a.pool_v + dst, vv);
+            }
+        }
+
         if constexpr (KG == 2) {
             // ---- group 1 hands its (m, l, O) to group 0 through the ring's
             //      LDS (every wave is past its last read of the ring).
@@ -620,21 +650,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
             }
         }
 
-        // ---- pages: this query block's own K/V rows, once per KV head.
-        if (a.pool_k) {
-            for (int idx = tid; idx < BM * CPR; idx += NTH) {
-                const int key = q0 + idx / CPR;
-                const int ch = idx % CPR;
-                if (key >= S || key / kPage >= a.max_pages) continue;
-                const int pid = a.bt[(int64_t)b * a.max_pages + key / kPage];
-                if (pid < 0 || pid >= a.num_pages) continue;
-                const int64_t dst =
-                    (((int64_t)kvh * a.num_pages + pid) * kPage + key % kPage) * D + 8 * ch;
-                store_half8(a.pool_k + dst, load_half8(kb + (int64_t)key * kvrs + 8 * ch));
-                store_half8(a.pool_v + dst, load_half8(vb + (int64_t)key * kvrs + 8 * ch));
-            }
-        }
-        wait_vmcnt<0>();   // page stores complete before the next ring starts
+        wait_vmcnt<0>();   // page and output stores complete before the next ring starts
     }
 }
 

@@ -93,7 +93,29 @@ def test_prefill_batched():
         assert_attn_close(got[i], ref, f"batch {i}")
 
 
-@pytest.mark.parametrize("s,hq,hkv,d", [(2048, 32, 8, 128), (333, 14, 2, 64), (70, 6, 3, 96)])
+# Short prompts with G <= 4 run one pass per pair of query blocks (the short
+# block's units first share key tiles with the long block, then help with the
+# long block's tiles).  Cases: G = 1 / 2 / 4, D = 64 / 128, odd block counts
+# (the middle pair is a single block), partial last tiles, a pair whose two
+# blocks end in the same tile, and a batch.
+@pytest.mark.parametrize("s,hq,hkv,d,batch", [
+    (1, 4, 4, 128, 1), (96, 4, 4, 128, 1), (333, 4, 4, 64, 1), (1000, 4, 4, 128, 1),
+    (100, 8, 4, 128, 1), (513, 8, 4, 64, 1), (640, 8, 4, 128, 1),
+    (33, 16, 4, 128, 1), (224, 16, 4, 64, 1), (777, 16, 4, 128, 2),
+])
+def test_prefill_pair_pass_full_check(s, hq, hkv, d, batch):
+    rng = np.random.default_rng(7 * s + hq + d)
+    q = oracle.normal_f16(rng, (batch, s, hq, d))
+    k, v = oracle.normal_f16(rng, (batch, s, hkv, d)), oracle.normal_f16(rng, (batch, s, hkv, d))
+    note(f"prefill pair pass S={s} Hq={hq} Hkv={hkv} D={d} B={batch}")
+    got = _prefill(q, k, v, hq, hkv, d, batch=batch)
+    for i in range(batch):
+        ref = oracle.causal_gqa(q[i].astype(np.float32), k[i].astype(np.float32),
+                                v[i].astype(np.float32), hq, hkv, d, nthreads=8)
+        assert_attn_close(got[i], ref, f"batch {i}")
+
+
+@pytest.mark.parametrize("s,hq,hkv,d", [(2048, 32, 8, 128), (333, 14, 2, 64), (70, 6, 3, 96), (515, 8, 4, 128), (200, 4, 4, 64)])
 def test_prefill_paged_writes_pages_bit_exact(s, hq, hkv, d):
     """flash_prefill_paged writes K/V rows into the pages exactly as the paged
     append does (config 4: K/V written into 16-token pages as produced)."""
