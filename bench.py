@@ -17,7 +17,8 @@ q read, out write, block-table and length reads; append: new K/V read + write)
 divided by the measured step time (host clock over the timed steps).
 roofline = that call (split kernel + merge kernel), timed by one HIP event
 pair on its stream around the timed region; also against the device's
-measured streaming-read ceiling (kvhp_stream_read over 2 GiB, flushed), and
+measured streaming-read ceiling (kvhp_stream_read over 2 GiB, flushed) and
+against the paged-read ceiling at the step's own size (kvhp_page_read), and
 beside it the same steps on one pool back to back and single flushed steps
 (median, min, max).
 cpu_baseline = the oracle's restatement of the reference CPU attention
@@ -117,6 +118,29 @@ def spread(t, nbytes=None):
     if nbytes:
         d["GB/s"] = round(nbytes / t[0] / 1e3, 1)
     return d
+
+
+def run_page_read(torch, kvhp, nbytes, page_bytes=4096, reps=25):
+    """Ceiling of a paged decode's page reads (kvhp_page_read): a dense pool of
+    nbytes read once in a seeded random page order, as the config-3 step
+    reads its pool; flushed before each rep, 5 warm-up and `reps` timed reps."""
+    n = max(1, nbytes // page_bytes)
+    pool = torch.ones((n * page_bytes) // 4, dtype=torch.float32, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    ids = torch.from_numpy(np.random.default_rng(7).permutation(n).astype(np.int32)).cuda()
+    fl = Flusher(torch)
+    for _ in range(5):
+        kvhp.page_read(pool, ids, page_bytes, sink)
+    t = time_op(torch, lambda: kvhp.page_read(pool, ids, page_bytes, sink), reps, fl)
+    rb = n * page_bytes
+    del pool, fl
+    torch.cuda.empty_cache()
+    return {"GBps": round(rb / t[0] / 1e3, 1), "GBps_best": round(rb / t[2] / 1e3, 1),
+            "GBps_worst": round(rb / t[3] / 1e3, 1), "bytes": rb, "pages": n,
+            "page_bytes": page_bytes, "reps": reps,
+            "pct_of_spec": round(rb / t[0] / 1e3 / HBM_PEAK_GBS * 100, 1),
+            "kernel": "page_read_kernel (kvhp_page_read), dense pool in random page order, "
+                      "flushed"}
 
 
 def run_stream_read(torch, kvhp, gib=2, reps=25):
@@ -740,6 +764,8 @@ def main():
     sbytes = r["step_bytes"]
     achieved = sbytes / r["step_us_region"] / 1e3
     fl_step, fl_sep, fl_dec = r["step_flushed"], r["separate_flushed"], r["decode_only_flushed"]
+    log("paged-read ceiling ...")
+    pr = run_page_read(torch, kvhp, dbytes)
     line = {
         "metric": METRIC,
         "value": round(r["value"], 2),
@@ -777,6 +803,8 @@ def main():
                                            "max": round(r["step_us_max"], 2)},
                      "stream_read": sr,
                      "frac_of_stream_read": round(achieved / sr["GBps"], 4),
+                     "paged_read": pr,
+                     "frac_of_paged_read": round(achieved / pr["GBps"], 4),
                      "same_pool_back_to_back_us": round(r["same_pool_us_region"], 2),
                      "same_pool_back_to_back_GBps": round(sbytes / r["same_pool_us_region"] / 1e3, 1),
                      "flushed": {**spread(fl_step, sbytes),
@@ -789,7 +817,10 @@ def main():
                              "flushed = single steps after a 512 MB write + 1 GiB read (median, "
                              "min, max of 10); separate = the step as kvhp_paged_append_kv + "
                              "kvhp_decode_attention; stream_read = the device's streaming-read "
-                             "ceiling (kvhp_stream_read over 2 GiB, flushed)"},
+                             "ceiling (kvhp_stream_read over 2 GiB, flushed); paged_read = a "
+                             "dense pool of the decode's size read once in a random 4 KB page "
+                             "order (kvhp_page_read, flushed): the ceiling of the step's page "
+                             "reads at its size"},
     }
     if not args.no_cpu:
         log("cpu baseline ...")

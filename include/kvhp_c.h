@@ -84,6 +84,18 @@ const char* kvhp_build_id(void);
  * to get the device's achievable read bandwidth. */
 int kvhp_stream_read(const void* buf, size_t bytes, void* sink, void* stream);
 
+/* Paged-read calibration beside the streaming probe above (the same
+ * reference probe, src/cuda/read_bandwidth.cu:8-118, for the access pattern
+ * of a paged decode): reads the pages page_ids[0..n_ids) of `pool`
+ * (pool_bytes of device memory cut into pages of page_bytes = 2048 or 4096,
+ * the page of one KV head at D = 64 or 128) once each with 16-byte
+ * non-temporal loads; ids outside the pool are clamped into it.  Writes
+ * nothing but possibly the 4-byte sink, as above.  With a random page order
+ * and as many pages as a decode step reads, its rate is the ceiling of that
+ * step's page reads. */
+int kvhp_page_read(const void* pool, int64_t pool_bytes, const int32_t* page_ids, int64_t n_ids,
+                   int page_bytes, void* sink, void* stream);
+
 /* Replaces engine::cuda::append_kv_cache (src/runtime/kv_cache.h:80-91,
  * kernel src/runtime/kv_cache.cu:8-61).  src [num_tokens][Hkv][D] token-major
  * -> dst head base [Hkv][max_seq][D] at positions start_pos.., positions

@@ -1,15 +1,22 @@
-// bandwidth.hip -- streaming-read calibration (the reference's read-bandwidth
+// bandwidth.hip -- read-bandwidth calibration (the reference's read-bandwidth
 // probe, src/cuda/read_bandwidth.cu:8-118, which calibrates its decode
 // ceilings, docs/GATES.md:21).
 //
 // stream_read_kernel reads every 16-byte chunk of a buffer once with
-// non-temporal loads, four chunks in flight per lane, grid-stride, and folds
-// them into one word per lane that is stored only if it equals a fixed
-// constant (so the loads cannot be dropped and nothing is written in
-// practice).  Its rate over a buffer far larger than the 256 MB MALL, with
-// the caches flushed before it, is the read ceiling an HBM-bound kernel can
-// reach on the device; the bench reports decode bytes against it beside the
-// 8 TB/s specification.
+// non-temporal loads: each workgroup streams its own contiguous share, eight
+// 16-byte chunks in flight per lane (adjacent 4 KB blocks of the workgroup),
+// and folds them into one word per lane that is stored only if it equals a
+// fixed constant (so the loads cannot be dropped and nothing is written in
+// practice).  Measured over 2 GiB on MI355X: a grid-stride loop (consecutive
+// lanes adjacent, a lane's loads a grid apart, as the reference's probe)
+// reaches ~5.9 TB/s, per-workgroup contiguous shares ~6.9-7.0 TB/s, and plain
+// (temporal) loads ~1 TB/s less than non-temporal ones; the contiguous form
+// is the device's streaming-read ceiling.
+//
+// page_read_kernel reads a list of pages (2 or 4 KB, the page of one KV head
+// at D = 64 or 128) in list order, one wave per workgroup, four pages in
+// flight per wave: the ceiling of a paged decode that reads the same pages
+// in a random order.
 #include "kvhp_internal.h"
 
 #include <algorithm>
@@ -20,22 +27,56 @@ namespace {
 constexpr int kReadThreads = 256;
 constexpr uint32_t kSinkMagic = 0x9E3779B9u;
 
+constexpr int kReadDepth = 8;   // 16-byte chunks in flight per lane
+
 __global__ void __launch_bounds__(kReadThreads)
 stream_read_kernel(const u32x4* p, size_t n16, uint32_t* sink) {
-    const size_t stride = (size_t)gridDim.x * kReadThreads;
-    size_t i = (size_t)blockIdx.x * kReadThreads + threadIdx.x;
+    const size_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const size_t beg = (size_t)blockIdx.x * per;
+    const size_t end = beg + per < n16 ? beg + per : n16;
+    size_t i = beg + threadIdx.x;
     uint32_t acc = 0;
-    for (; i + 3 * stride < n16; i += 4 * stride) {
-        const u32x4 a = __builtin_nontemporal_load(p + i);
-        const u32x4 b = __builtin_nontemporal_load(p + i + stride);
-        const u32x4 c = __builtin_nontemporal_load(p + i + 2 * stride);
-        const u32x4 d = __builtin_nontemporal_load(p + i + 3 * stride);
-        acc ^= (a[0] ^ b[1] ^ c[2] ^ d[3]) + (a[1] ^ b[2] ^ c[3] ^ d[0]) +
-               (a[2] ^ b[3] ^ c[0] ^ d[1]) + (a[3] ^ b[0] ^ c[1] ^ d[2]);
+    for (; i + (kReadDepth - 1) * kReadThreads < end; i += kReadDepth * kReadThreads) {
+        u32x4 v[kReadDepth];
+#pragma unroll
+        for (int j = 0; j < kReadDepth; ++j) v[j] = __builtin_nontemporal_load(p + i + j * kReadThreads);
+#pragma unroll
+        for (int j = 0; j < kReadDepth; ++j) acc ^= (v[j][0] + v[j][1]) ^ (v[j][2] + v[j][3] + j);
     }
-    for (; i < n16; i += stride) {
+    for (; i < end; i += kReadThreads) {
         const u32x4 a = __builtin_nontemporal_load(p + i);
         acc ^= a[0] + a[1] + a[2] + a[3];
+    }
+    if (acc == kSinkMagic) *sink = acc;
+}
+
+constexpr int kPagesInFlight = 4;
+
+// LPP: 1 KB wave loads per page (2: 2 KB pages, 4: 4 KB pages).  Wave w reads
+// list entries [w*per, (w+1)*per); ids outside the pool are clamped into it.
+template <int LPP>
+__global__ void __launch_bounds__(kWave)
+page_read_kernel(const u32x4* pool, int64_t pool_pages, const int32_t* ids, int64_t n_ids,
+                 int64_t per, uint32_t* sink) {
+    const int lane = threadIdx.x;
+    const int64_t beg = (int64_t)blockIdx.x * per;
+    const int64_t end = beg + per < n_ids ? beg + per : n_ids;
+    uint32_t acc = 0;
+    for (int64_t i = beg; i < end; i += kPagesInFlight) {
+        u32x4 v[kPagesInFlight][LPP];
+#pragma unroll
+        for (int j = 0; j < kPagesInFlight; ++j) {
+            const int64_t e = i + j < end ? i + j : end - 1;
+            int64_t id = ids[e];
+            id = id < 0 ? 0 : (id >= pool_pages ? pool_pages - 1 : id);
+            const u32x4* pg = pool + id * (LPP * kWave);
+#pragma unroll
+            for (int r = 0; r < LPP; ++r) v[j][r] = __builtin_nontemporal_load(pg + r * kWave + lane);
+        }
+#pragma unroll
+        for (int j = 0; j < kPagesInFlight; ++j)
+#pragma unroll
+            for (int r = 0; r < LPP; ++r) acc ^= (v[j][r][0] + v[j][r][1]) ^ (v[j][r][2] + v[j][r][3] + j);
     }
     if (acc == kSinkMagic) *sink = acc;
 }
@@ -62,4 +103,35 @@ extern "C" int kvhp_stream_read(const void* buf, size_t bytes, void* sink, void*
                        0, static_cast<hipStream_t>(stream), static_cast<const u32x4*>(buf), n16,
                        static_cast<uint32_t*>(sink));
     return check_launch("stream_read");
+}
+
+extern "C" int kvhp_page_read(const void* pool, int64_t pool_bytes, const int32_t* page_ids,
+                              int64_t n_ids, int page_bytes, void* sink, void* stream) {
+    clear_error();
+    if (n_ids <= 0) return KVHP_OK;
+    KVHP_REQUIRE(pool && page_ids && sink, KVHP_ERR_INVALID, "page_read: null pointer");
+    KVHP_REQUIRE(aligned16(pool), KVHP_ERR_INVALID, "page_read: pool not 16-byte aligned");
+    KVHP_REQUIRE(page_bytes == 2048 || page_bytes == 4096, KVHP_ERR_UNSUPPORTED,
+                 "page_read: page_bytes %d is neither 2048 nor 4096", page_bytes);
+    const int64_t pool_pages = pool_bytes / page_bytes;
+    KVHP_REQUIRE(pool_pages > 0, KVHP_ERR_INVALID, "page_read: pool smaller than a page");
+    int dev = 0, cus = 0;
+    KVHP_HIP(hipGetDevice(&dev), "hipGetDevice");
+    KVHP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+             "hipDeviceGetAttribute");
+    // eight waves per CU, each a contiguous share of the list
+    const int64_t want = (int64_t)(cus > 0 ? cus : 256) * 8;
+    const int64_t waves = std::min<int64_t>(want, (n_ids + kPagesInFlight - 1) / kPagesInFlight);
+    const int64_t per = (n_ids + waves - 1) / waves;
+    const int64_t grid = (n_ids + per - 1) / per;
+    auto* p = static_cast<const u32x4*>(pool);
+    auto* sk = static_cast<uint32_t*>(sink);
+    auto s = static_cast<hipStream_t>(stream);
+    if (page_bytes == 4096)
+        hipLaunchKernelGGL(page_read_kernel<4>, dim3(static_cast<unsigned>(grid)), dim3(kWave), 0, s,
+                           p, pool_pages, page_ids, n_ids, per, sk);
+    else
+        hipLaunchKernelGGL(page_read_kernel<2>, dim3(static_cast<unsigned>(grid)), dim3(kWave), 0, s,
+                           p, pool_pages, page_ids, n_ids, per, sk);
+    return check_launch("page_read");
 }

@@ -74,6 +74,7 @@ _SIGNATURES = {
                                      _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
     "kvhp_build_id": (ctypes.c_char_p, []),
     "kvhp_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
+    "kvhp_page_read": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _vp]),
     "kvhp_decode_attention_noalloc": (_i32, [_vp, ctypes.POINTER(KVView), ctypes.POINTER(KVView),
                                              _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "kvhp_paged_append_decode": (_i32, [_vp, _vp, _vp, ctypes.POINTER(KVView),
@@ -135,6 +136,13 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     if not os.path.exists(path):
         raise FileNotFoundError(
             f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+    # torch's HIP runtime first, so that the library binds to the same one:
+    # loaded the other way round, the process holds two HIP runtimes and the
+    # library's finds no device once torch's has opened it.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     for name, (res, args) in _SIGNATURES.items():
         fn = getattr(lib, name)
@@ -174,6 +182,14 @@ def stream_read(buf, sink, stream=None):
     device tensor of at least 4 bytes."""
     _check(load().kvhp_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
                                    _stream(stream)))
+
+
+def page_read(pool, page_ids, page_bytes, sink, stream=None):
+    """Read the pages page_ids (int32 device tensor) of the device tensor
+    `pool` cut into pages of page_bytes (kvhp_page_read); sink: a 4-byte
+    device tensor."""
+    _check(load().kvhp_page_read(_ptr(pool), pool.numel() * pool.element_size(), _ptr(page_ids),
+                                 page_ids.numel(), page_bytes, _ptr(sink), _stream(stream)))
 
 
 def last_error() -> str:
