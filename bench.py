@@ -376,7 +376,52 @@ def run_config3(torch, kvhp, args):
         step_on(insts[i % R])
     torch.cuda.synchronize()
     n = args.steps
-    wall, region_us = timed(n, True)
+    # The timed steps as one HIP graph, replayed (a serving loop captures its
+    # decode step; the eager launches of the same steps are timed beside
+    # it).  The graph's outputs must equal an eager step's bit for bit.
+    graph, graph_ok = None, False
+    try:
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(stream)
+        with torch.cuda.graph(graph, stream=cap, capture_error_mode="thread_local"):
+            for i in range(n):
+                step_on(insts[i % R])
+        stream.wait_stream(cap)
+        torch.cuda.synchronize()
+        for ci in insts:
+            ci["out"].zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        from_graph = [ci["out"].clone() for ci in insts[:min(R, n)]]
+        for ci in insts[:min(R, n)]:
+            ci["out"].zero_()
+            step_on(ci)
+        torch.cuda.synchronize()
+        graph_ok = all(torch.equal(g_out, ci["out"]) for g_out, ci in zip(from_graph, insts))
+    except Exception as exc:  # capture unsupported here: eager launches only
+        log(f"config3 graph capture failed: {exc}")
+        graph = None
+    if graph is not None and not graph_ok:
+        log("config3 graph outputs differ from eager steps: timing eager launches")
+
+    def timed_graph():
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        graph.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, ev0.elapsed_time(ev1) * 1e3
+
+    eager_wall, eager_region_us = timed(n, True)
+    if graph is not None and graph_ok:
+        graph.replay()   # warm replay
+        wall, region_us = timed_graph()
+    else:
+        wall, region_us = eager_wall, eager_region_us
     # per-step spread, from a second pass with an event pair per step
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(n)]
@@ -392,6 +437,9 @@ def run_config3(torch, kvhp, args):
     res = {
         "ms_per_step": wall * 1e3 / n,
         "value": step_bytes / (wall / n) / 1e9,
+        "launch": "hip_graph" if (graph is not None and graph_ok) else "eager",
+        "eager_us_per_step": eager_wall * 1e6 / n,
+        "eager_us_region": eager_region_us / n,
         "step_us_region": region_us / n,
         "step_us_median": float(np.median(step_us)),
         "step_us_min": float(np.min(step_us)),
@@ -412,7 +460,7 @@ def run_config3(torch, kvhp, args):
     res["step_flushed"] = time_op(torch, step, 10, fl)
     res["separate_flushed"] = time_op(torch, lambda: (append(), decode()), 10, fl)
     res["decode_only_flushed"] = time_op(torch, decode, 10, fl)
-    del fl
+    del fl, graph
     for ci in insts[1:]:
         ci.clear()
     torch.cuda.empty_cache()
@@ -789,7 +837,9 @@ def main():
                         "(seed 3), 32 q / 8 KV heads, D=128, 16-token pages, random-permutation "
                         "block tables; step = paged append 1 token/seq + split-K decode; steps "
                         f"rotate over {r['pools']} separately allocated input copies (no step "
-                        "reuses the previous step's data from the 256 MB MALL)",
+                        "reuses the previous step's data from the 256 MB MALL); the timed steps "
+                        "are replayed as one HIP graph (launch = hip_graph; eager launches "
+                        "beside)",
             "sum_L": r["sum_L"], "splits": r["splits"], "decode_bytes": dbytes,
             "step_bytes": r["step_bytes"], "pools": r["pools"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
@@ -805,6 +855,11 @@ def main():
                      "frac_of_stream_read": round(achieved / sr["GBps"], 4),
                      "paged_read": pr,
                      "frac_of_paged_read": round(achieved / pr["GBps"], 4),
+                     "launch": r["launch"],
+                     "eager": {"us_per_step": round(r["eager_us_per_step"], 2),
+                               "us_region": round(r["eager_us_region"], 2),
+                               "GBps": round(sbytes / r["eager_us_per_step"] / 1e3, 1),
+                               "frac": round(sbytes / r["eager_us_region"] / 1e3 / HBM_PEAK_GBS, 4)},
                      "same_pool_back_to_back_us": round(r["same_pool_us_region"], 2),
                      "same_pool_back_to_back_GBps": round(sbytes / r["same_pool_us_region"] / 1e3, 1),
                      "flushed": {**spread(fl_step, sbytes),
@@ -813,7 +868,8 @@ def main():
                      "decode_only_flushed": spread(fl_dec, dbytes),
                      "note": "achieved = algorithmic bytes of the step / (HIP-event time of the "
                              "timed region / steps), one call per step, steps rotating over the "
-                             "input copies; same_pool = the steps back to back on one copy; "
+                             "input copies and replayed from one HIP graph (eager = the same "
+                             "steps launched one by one); same_pool = the steps back to back on one copy; "
                              "flushed = single steps after a 512 MB write + 1 GiB read (median, "
                              "min, max of 10); separate = the step as kvhp_paged_append_kv + "
                              "kvhp_decode_attention; stream_read = the device's streaming-read "

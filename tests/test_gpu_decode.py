@@ -459,3 +459,72 @@ def test_decode_row_pitch_beyond_24_bits(stride_s):
     assert_attn_close(from_gpu(out).astype(np.float32), ref, f"stride_s={stride_s}")
     del kt, vt
     torch.cuda.empty_cache()
+
+
+def test_paged_append_decode_graph_replays():
+    """The serving step (kvhp_paged_append_decode) captured in a HIP graph, as
+    the bench times it: two batches (ragged, 40 sequences: the balanced
+    split list) in one graph over a shared workspace, replayed three times
+    with new queries each time and an eager step of a third batch on the
+    same workspace between the replays; every replay's outputs and pools
+    equal the eager call's bit for bit."""
+    import torch
+    rng = np.random.default_rng(909)
+    hq, hkv, d = 32, 8, 128
+
+    def batch(seed_lens):
+        lens = rng.integers(0, 3000, size=40).astype(np.int32)
+        lens[:3] = seed_lens
+        b = lens.size
+        bt, P = make_block_tables(rng, lens + 8)
+        return {"b": b, "bt": to_gpu(bt), "pos": to_gpu(lens), "seq": to_gpu(lens + 1),
+                "cap": int(lens.max()) + 1,
+                "pk": to_gpu_f16(oracle.normal_f16(rng, (hkv, P, 16, d))),
+                "pv": to_gpu_f16(oracle.normal_f16(rng, (hkv, P, 16, d))),
+                "kn": to_gpu_f16(oracle.normal_f16(rng, (b, hkv, d))),
+                "vn": to_gpu_f16(oracle.normal_f16(rng, (b, hkv, d))),
+                "q": to_gpu_f16(oracle.normal_f16(rng, (b, hq, d))),
+                "out": torch.zeros((b, hq, d), dtype=torch.float16, device="cuda")}
+
+    A, B, C = batch([0, 16, 2999]), batch([1, 15, 64]), batch([7, 300, 2048])
+    cap = max(x["cap"] for x in (A, B, C))
+    ws = torch.zeros(kvhp.decode_workspace_bytes(40, hq, hkv, d, cap), dtype=torch.uint8,
+                     device="cuda")
+
+    def step(x, pk=None, pv=None, out=None):
+        pk = x["pk"] if pk is None else pk
+        pv = x["pv"] if pv is None else pv
+        out = x["out"] if out is None else out
+        kvhp.paged_append_decode(x["q"], x["kn"], x["vn"], kvhp.paged_view(pk, x["bt"]),
+                                 kvhp.paged_view(pv, x["bt"]), x["pos"], x["seq"], out, hq, hkv,
+                                 d, cap, 0, ws)
+
+    step(A)
+    step(B)
+    sync()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+        step(A)
+        step(B)
+    torch.cuda.current_stream().wait_stream(s)
+    sync()
+    for r in range(3):
+        note(f"graph replay {r}")
+        for x in (A, B):
+            x["q"].copy_(to_gpu_f16(oracle.normal_f16(rng, (x["b"], hq, d))))
+            x["out"].fill_(float("nan"))
+        g.replay()
+        sync()
+        for x in (A, B):
+            # the append is idempotent (same rows at the same positions), so
+            # the eager call on copies of the current pools is the reference
+            pk, pv = x["pk"].clone(), x["pv"].clone()
+            ref = torch.full_like(x["out"], float("nan"))
+            step(x, pk, pv, ref)
+            sync()
+            assert torch.equal(ref, x["out"]), f"replay {r}: outputs differ"
+            assert torch.equal(pk, x["pk"]) and torch.equal(pv, x["pv"]), f"replay {r}: pools differ"
+        step(C)   # other work on the same workspace between the replays
+        sync()
