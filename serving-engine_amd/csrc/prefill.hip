@@ -8,7 +8,8 @@
 // tile is read from HBM once per workgroup and consumed by all 8 waves, so
 // GQA heads share their K/V traffic.  Query blocks i and N-1-i are processed
 // by the same workgroup (two passes), giving every workgroup the same causal
-// work; grid x enumerates (pair, kv_head) with the kv head fastest.
+// work (short prompts: odd KV heads run the long block first); grid x
+// enumerates (pair, kv_head) with the kv head fastest.
 //
 // K/V staging: a 4-stage LDS ring (4 x 32 KB for D=128), filled by
 // global_load_lds_dwordx4 (direct HBM->LDS, no VGPR round trip).  Tile t+3 is
@@ -256,8 +257,13 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
 
     for (int pass = 0; pass < 2; ++pass) {
-        const int qblk = pass == 0 ? pair : a.n_qblk - 1 - pair;
-        if (pass == 1 && qblk <= pair) break;   // odd count: middle block once
+        // Short prompts: odd KV heads (other XCDs) take their long block
+        // first, so that half the workgroups load Q and drain stores while
+        // the other half run tile loops (every workgroup of a KV head still
+        // walks the same tiles together).
+        const bool flip = KG == 2 && (kvh & 1) != 0;
+        const int qblk = (pass == 0) != flip ? pair : a.n_qblk - 1 - pair;
+        if (pass == 1 && a.n_qblk - 1 - pair <= pair) break;   // odd count: middle block once
         const int q0 = qblk * BM;
 
         // ---- this wave's unit: head kvh*G + u%G, rows r0 .. r0+31; its key
