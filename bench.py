@@ -28,11 +28,13 @@ Also reported under "extra" (each measured with L2+MALL flushed by a 512 MB
 write and a 1 GiB read before every rep unless labelled warm; median, min and
 max): config 1 (decode at ctx 512), config 2 (ctx 4K/16K/64K x splits
 1/4/16/64, also against the streaming-read ceiling), config 4 (causal prefill
-S=512/2048/8192, TFLOP/s vs fp16 MFMA peak), config 5 (Llama-style 1.1B:
+S=512/2048/8192 writing the K/V pages, TFLOP/s vs fp16 MFMA peak, the
+attention alone beside it), config 5 (Llama-style 1.1B:
 2048-id prefill, then 128 greedy decode steps, tok/s and the HBM bytes of a
-step against 8 TB/s; also top-level as config5_decode_tok_s), and the KV
-movement kernels alone (paged gather of the config-3 pool, 2048-token
-appends).  The line carries the library's build id (source hash) and whether
+step against 8 TB/s; also top-level as config5_decode_tok_s), the same
+model serving 8 and 32 sequences per step through the batched runner
+(ctx 2048, eager launches, tok/s), and the KV movement kernels alone (paged
+gather of the config-3 pool, 2048-token appends).  The line carries the library's build id (source hash) and whether
 it matches the sources in the tree.
 """
 import argparse
@@ -66,7 +68,7 @@ def parse():
                          "over (504 MB each)")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 2 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5,kv")
+    ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5,c5b,kv")
     ap.add_argument("--profile", nargs="?", const="decode", default=None,
                     choices=("decode", "prefill", "c5", "batched"),
                     help="short run for rocprofv3: a 256 MiB device copy (counter "
@@ -884,7 +886,7 @@ def main():
     del c
     torch.cuda.empty_cache()
     extra = {}
-    parts = set(args.only.split(",")) if args.only else {"c1", "c2", "c4", "c5", "kv"}
+    parts = set(args.only.split(",")) if args.only else {"c1", "c2", "c4", "c5", "c5b", "kv"}
     if not args.no_extra:
         if "kv" in parts:
             log("kv movement ...")
@@ -905,6 +907,9 @@ def main():
             if not args.no_cpu:
                 log("config5 cpu baseline ...")
                 extra["config5"]["cpu_baseline"] = cpu_baseline_config5(torch, kvhp)
+        if "c5b" in parts:
+            log("config5 batched runner ...")
+            extra["config5_batched"] = run_config5_batched(torch, kvhp, batches=(8, 32), steps=20)
     line["extra"] = extra
     print(json.dumps(line))
 
