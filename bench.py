@@ -725,7 +725,7 @@ def run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=20, ctx=2048):
     cfg = kvhp.llama_1b_config()
     L, hkv, d, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
     bmax = max(batches)
-    per = (ctx + steps + 8 + 15) // 16
+    per = (ctx + 3 * steps + 24 + 15) // 16   # eager steps, then the graph's
     P = bmax * per
     model = kvhp.LlamaModel(cfg, seed=5, max_ctx=max(ctx, bmax))
     pool = torch.zeros(L * 2 * hkv * P * 16 * d, dtype=torch.float16, device="cuda")
@@ -752,9 +752,53 @@ def run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=20, ctx=2048):
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
-        out[f"B{B}"] = {"ms_per_step": round(ms, 4), "tok_s": round(B * 1e3 / ms, 1)}
+        res = {"ms_per_step": round(ms, 4), "tok_s": round(B * 1e3 / ms, 1)}
+        # The same steps captured as one HIP graph and replayed (positions
+        # of every step in device memory at fixed addresses; the attention
+        # planned for the last step's length); the graph's last logits must
+        # equal an eager step's bit for bit.
+        base = ctx + 3 + steps
+        pos_all = torch.tensor([[base + i] * B for i in range(steps)], dtype=torch.int32,
+                               device="cuda")
+        seq_all = pos_all + 1
+        cap_len = base + steps
+
+        def gstep(i, lg):
+            model.decode_paged(toks, pool, P, bt[:B], per, pos_all[i], seq_all[i], cap_len, lg,
+                               nxt[:B])
+        try:
+            for i in range(2):
+                gstep(i, logits[:B])
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            cs = torch.cuda.Stream()
+            cs.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.graph(g, stream=cs, capture_error_mode="thread_local"):
+                for i in range(steps):
+                    gstep(i, logits[:B])
+            torch.cuda.current_stream().wait_stream(cs)
+            g.replay()
+            torch.cuda.synchronize()
+            ref = torch.empty_like(logits[:B])
+            gstep(steps - 1, ref)
+            torch.cuda.synchronize()
+            same = torch.equal(ref, logits[:B])
+            if same:
+                e0.record()
+                g.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                gms = e0.elapsed_time(e1) / steps
+                res["graph"] = {"ms_per_step": round(gms, 4), "tok_s": round(B * 1e3 / gms, 1)}
+            else:
+                res["graph"] = {"error": "graph logits differ from an eager step"}
+            del g
+        except Exception as exc:  # capture unsupported here: eager figure only
+            res["graph"] = {"error": str(exc)[:200]}
+        out[f"B{B}"] = res
     model.close()
-    return {"workload": f"config-5 model, batched runner, ctx {ctx}, eager launches", **out}
+    return {"workload": f"config-5 model, batched runner, ctx {ctx}; eager launches, and the "
+                        "same steps replayed from one HIP graph (graph)", **out}
 
 
 def traffic_from_profile(dbytes):
