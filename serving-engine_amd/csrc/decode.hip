@@ -1,11 +1,15 @@
 // decode.hip -- split-K decode attention over a GQA fp16 KV cache (gfx950).
 //
-// Work decomposition: one 64-lane workgroup per (split, kv_head, sequence).
-// A split is a page-aligned chunk of `chunk` tokens (a multiple of 64; at
-// most 64 pages with a block table); the workgroup serves all G = Hq/Hkv
-// query heads of its KV head, so every K/V byte is read from HBM exactly once
-// (the reference re-reads each KV row once per query head,
-// src/cuda/decode_attention_split.cu:40-49).
+// Work decomposition: one workgroup per (split, kv_head, sequence).  A split
+// is a page-aligned chunk of `chunk` tokens (a multiple of 64; at most 64
+// pages with a block table); the workgroup serves all G = Hq/Hkv query heads
+// of its KV head, so every K/V byte is read from HBM exactly once (the
+// reference re-reads each KV row once per query head,
+// src/cuda/decode_attention_split.cu:40-49).  Balanced batches (below) run
+// one wave per split.  Fixed chunks at D = 64, and single splits, run four
+// waves per split that take its 32-token steps round robin and fold their
+// (m, l, O) together in LDS: each wave's chain of dependent steps (~0.55 us
+// each with one wave per CU) is a quarter as long.
 //
 // Per 32-token step (2 pages of 16 tokens), both contractions run on
 // v_mfma_f32_16x16x32_f16 in transposed form, so that lane (g, col) owns
@@ -26,7 +30,8 @@
 // throughput), then staged through LDS: K back in the A layout, V for the
 // transposed reads.  Non-temporal loads (the cache is streamed once) and
 // identical loads on every path so the compiler keeps exact vmcnt waits.
-// 252 VGPRs and 17.9 KB LDS at D=128: two waves per SIMD, eight per CU.
+// Up to 252 VGPRs and 17.9 KB LDS per wave at D=128: two waves per SIMD,
+// eight per CU.
 //
 // Splits: a sequence whose keys fit one split gets its output written
 // directly; otherwise each split stores (m, l, o[D]) in fp32 and
@@ -159,10 +164,11 @@ __device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
 // K runs two steps ahead in registers, V one step; both are loaded as whole
 // rows and staged through LDS (K for the A layout, V for the transposed
 // reads).
-template <int D, int G, bool PAGED>
-__global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2)))
+template <int D, int G, bool PAGED, int W>
+__global__ void __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_splitk_kernel(const DecodeArgs a) {
     static_assert(G >= 1 && G <= 16, "one MFMA column per query head");
+    static_assert(W == 1 || W == 4, "one or four waves per split");
     constexpr int TOK = 32;          // tokens per step: 2 pages, one PV k-step
     constexpr int NC = D / 32;       // QK k-chunks
     constexpr int ND = D / 16;       // 16-dim output blocks
@@ -172,14 +178,18 @@ decode_splitk_kernel(const DecodeArgs a) {
     constexpr int VP = D + 16;       // V tile row pitch in halfs (bank skew)
     constexpr int KP = D + 8;        // K tile row pitch in halfs (bank skew)
 
-    __shared__ __attribute__((aligned(16))) f16 v_lds[TOK * VP];
-    __shared__ __attribute__((aligned(16))) f16 k_lds[TOK * KP];
+    __shared__ __attribute__((aligned(16))) f16 v_lds_all[W][TOK * VP];
+    __shared__ __attribute__((aligned(16))) f16 k_lds_all[W][TOK * KP];
 
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+    // W waves split the split's 32-token steps round robin and meet in LDS.
+    const int wv = W > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
+    f16* const v_lds = v_lds_all[wv];
+    f16* const k_lds = k_lds_all[wv];
     const int g = lane >> 4;
     const int col = lane & 15;
     int kvh, b, split, L, chunk;
-    if (a.balance > 0) {
+    if (W == 1 && a.balance > 0) {
         // Balanced work list: blockIdx.y is the index of this split among
         // all splits of the batch in sequence order (sequences without keys
         // keep one, which writes their zero output), blockIdx.x the kv head,
@@ -399,7 +409,7 @@ decode_splitk_kernel(const DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < NVL; ++j)
             *reinterpret_cast<half8*>(&k_lds[(RPL * j + vrow) * KP + vdim]) = kbuf[S][j];
-        if constexpr (PFK) load_k(S_, T0 + 2 * TOK);
+        if constexpr (PFK) load_k(S_, T0 + 2 * W * TOK);
         floatx4 C[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -444,7 +454,7 @@ decode_splitk_kernel(const DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < NVL; ++j)
             *reinterpret_cast<half8*>(&v_lds[(RPL * j + vrow) * VP + vdim]) = vbuf[j];
-        if constexpr (PFV) load_v(T0 + TOK);
+        if constexpr (PFV) load_v(T0 + W * TOK);
 
         // Rescale O only when some head's running max moved.
         if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.f)) {
@@ -467,24 +477,59 @@ decode_splitk_kernel(const DecodeArgs a) {
     using I1 = std::integral_constant<int, 1>;
     using Pf = std::true_type;
     using NoPf = std::false_type;
-    load_k(I0{}, t_begin);
-    load_v(t_begin);
-    load_k(I1{}, t_begin + TOK);
-    int it = 0;
-    for (; it + 3 < n_iter; it += 2) {
-        step(I0{}, Pf{}, Pf{}, it);
-        step(I1{}, Pf{}, Pf{}, it + 1);
+    // This wave's steps: wv, wv + W, wv + 2W, ... (n_w of them).
+    const int n_w = n_iter > wv ? (n_iter - wv + W - 1) / W : 0;
+    if (n_w > 0) {
+        const int s0 = t_begin + TOK * wv;
+        load_k(I0{}, s0);
+        load_v(s0);
+        load_k(I1{}, s0 + W * TOK);
+        int j = 0;
+        for (; j + 3 < n_w; j += 2) {
+            step(I0{}, Pf{}, Pf{}, wv + W * j);
+            step(I1{}, Pf{}, Pf{}, wv + W * (j + 1));
+        }
+        // tail: at most three steps, no loads past the split
+        if (j + 2 < n_w) {
+            step(I0{}, Pf{}, Pf{}, wv + W * j);
+            step(I1{}, NoPf{}, Pf{}, wv + W * (j + 1));
+            step(I0{}, NoPf{}, NoPf{}, wv + W * (j + 2));
+        } else if (j + 1 < n_w) {
+            step(I0{}, NoPf{}, Pf{}, wv + W * j);
+            step(I1{}, NoPf{}, NoPf{}, wv + W * (j + 1));
+        } else {
+            step(I0{}, NoPf{}, NoPf{}, wv + W * j);
+        }
     }
-    // tail: at most three steps, no loads past the split
-    if (it + 2 < n_iter) {
-        step(I0{}, Pf{}, Pf{}, it);
-        step(I1{}, NoPf{}, Pf{}, it + 1);
-        step(I0{}, NoPf{}, NoPf{}, it + 2);
-    } else if (it + 1 < n_iter) {
-        step(I0{}, NoPf{}, Pf{}, it);
-        step(I1{}, NoPf{}, NoPf{}, it + 1);
-    } else {
-        step(I0{}, NoPf{}, NoPf{}, it);
+
+    if constexpr (W > 1) {
+        // ---- the W waves' (m, l, O) meet in LDS: waves 1.. write theirs
+        //      into their own K tile (free now: 64 (D + 8) bytes, exactly
+        //      D/4 + 2 floats per lane), wave 0 folds them in.
+        float* xs = reinterpret_cast<float*>(k_lds);
+        if (wv > 0) {
+#pragma unroll
+            for (int db = 0; db < ND; ++db)
+                *reinterpret_cast<floatx4*>(&xs[(db * kWave + lane) * 4]) = o[db];
+            xs[ND * kWave * 4 + 2 * lane] = m_run;
+            xs[ND * kWave * 4 + 2 * lane + 1] = l_part;
+        }
+        __syncthreads();
+        if (wv > 0) return;
+#pragma unroll
+        for (int w = 1; w < W; ++w) {
+            const float* xw = reinterpret_cast<const float*>(k_lds_all[w]);
+            const float mw = xw[ND * kWave * 4 + 2 * lane];
+            const float lw = xw[ND * kWave * 4 + 2 * lane + 1];
+            const float mn = fmaxf(m_run, mw);
+            const float a0 = fast_exp2((m_run - mn) * sc);
+            const float a1 = fast_exp2((mw - mn) * sc);
+            l_part = l_part * a0 + lw * a1;
+#pragma unroll
+            for (int db = 0; db < ND; ++db)
+                o[db] = o[db] * a0 + *reinterpret_cast<const floatx4*>(&xw[(db * kWave + lane) * 4]) * a1;
+            m_run = mn;
+        }
     }
 
     const float l_tot = rows4_sum(l_part);
@@ -710,6 +755,10 @@ Plan make_plan(int batch, int num_kv_heads, int max_seq_len, int num_splits) {
         s = (max_seq_len + per_split - 1) / per_split;
         const int64_t grid_cap = units >= 6144 ? 1 : 6144 / units;
         if (s > grid_cap) s = static_cast<int>(grid_cap);
+        // Small batches up to 512 keys: one split (four waves of at most four
+        // 32-key steps each) and no merge launch, which costs more (~3 us)
+        // than the three steps it saves a wave (~0.55 us each).
+        if (batch < 8 && max_seq_len <= 512) s = 1;
     }
     if (s > max_by_chunk) s = max_by_chunk;
     if (s < 1) s = 1;
@@ -833,8 +882,8 @@ void launch_fast(const DecodeArgs& args, dim3 grid, bool paged, hipStream_t s) {
         // Balanced splits: about one split per resident wave slot over the
         // batch, less half a split per sequence for the rounding up of each
         // sequence's split count.
-        const int slots = paged ? resident_splits(decode_splitk_kernel<D, G, true>)
-                                : resident_splits(decode_splitk_kernel<D, G, false>);
+        const int slots = paged ? resident_splits(decode_splitk_kernel<D, G, true, 1>)
+                                : resident_splits(decode_splitk_kernel<D, G, false, 1>);
         a.balance = slots > 0 ? max(1, slots / a.Hkv - a.batch / 2) : 0;
         if (a.balance > 0) {
             // Work list of every split of the batch per kv head.  The split
@@ -849,10 +898,22 @@ void launch_fast(const DecodeArgs& args, dim3 grid, bool paged, hipStream_t s) {
                 a.balance = 0;
         }
     }
-    if (paged)
-        hipLaunchKernelGGL((decode_splitk_kernel<D, G, true>), grid, dim3(kWave), 0, s, a);
-    else
-        hipLaunchKernelGGL((decode_splitk_kernel<D, G, false>), grid, dim3(kWave), 0, s, a);
+    if (a.balance > 0) {   // the work list: one wave per split
+        if (paged)
+            hipLaunchKernelGGL((decode_splitk_kernel<D, G, true, 1>), grid, dim3(kWave), 0, s, a);
+        else
+            hipLaunchKernelGGL((decode_splitk_kernel<D, G, false, 1>), grid, dim3(kWave), 0, s, a);
+    } else if (D == 64 || a.nsplit == 1) {   // fixed chunks: four waves per split
+        if (paged)
+            hipLaunchKernelGGL((decode_splitk_kernel<D, G, true, 4>), grid, dim3(4 * kWave), 0, s, a);
+        else
+            hipLaunchKernelGGL((decode_splitk_kernel<D, G, false, 4>), grid, dim3(4 * kWave), 0, s, a);
+    } else {
+        if (paged)
+            hipLaunchKernelGGL((decode_splitk_kernel<D, G, true, 1>), grid, dim3(kWave), 0, s, a);
+        else
+            hipLaunchKernelGGL((decode_splitk_kernel<D, G, false, 1>), grid, dim3(kWave), 0, s, a);
+    }
     if (a.nsplit > 1)
         hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.Hkv, a.batch),
                            dim3(kMergeWaves * kWave), 0, s, a);

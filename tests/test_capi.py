@@ -34,10 +34,11 @@ def test_kv_view_struct_layout_matches_header():
 
 def test_auto_split_policy():
     # chunks of ~L/64 tokens but >= 128 (64-token multiples), grid of at most
-    # 6144 workgroups, never more than 256 splits
+    # 6144 workgroups, never more than 256 splits; batches below 8 with at
+    # most 512 keys: one split (no merge launch)
     assert kvhp.decode_auto_splits(1, 8, 128, 64) == 1
     expect = {(1, 8, 4096): 32, (1, 8, 16384): 64, (1, 8, 65536): 64, (1, 4, 2176): 17,
-              (1, 8, 512): 4, (32, 8, 8193): 22}
+              (1, 8, 512): 1, (7, 8, 512): 1, (8, 8, 512): 4, (1, 8, 513): 5, (32, 8, 8193): 22}
     for (b, hkv, L), want in expect.items():
         assert kvhp.decode_auto_splits(b, hkv, 128, L) == want, (b, hkv, L)
     for b, hkv, L in [(1, 8, 100), (3, 2, 600), (64, 8, 32768), (1, 1, 1 << 20), (256, 32, 4096)]:
