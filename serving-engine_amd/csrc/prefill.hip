@@ -8,8 +8,11 @@
 // tile is read from HBM once per workgroup and consumed by all 8 waves, so
 // GQA heads share their K/V traffic.  Query blocks i and N-1-i are processed
 // by the same workgroup (two passes), giving every workgroup the same causal
-// work (short prompts: odd KV heads run the long block first); grid x
-// enumerates (pair, kv_head) with the kv head fastest.
+// work (short prompts: odd KV heads run the long block first), when those
+// pairs fill the GPU; below that (S < 2048 at 32/8 heads) every block gets
+// its own workgroup, longest first, so that more CUs share the work (S=512
+// 15.4 vs 21.5 us).  Grid x enumerates (pair or block, kv_head) with the kv
+// head fastest.
 //
 // K/V staging: a 4-stage LDS ring (4 x 32 KB for D=128), filled by
 // global_load_lds_dwordx4 (direct HBM->LDS, no VGPR round trip).  Tile t+3 is
@@ -65,6 +68,7 @@ struct PrefillArgs {
     int S, Hq, Hkv, G;
     int RB;                 // 16-row blocks per query block (fast kernel)
     int n_qblk;
+    int paired;             // 1: query blocks i and n-1-i share a workgroup (two passes)
     float scale_log2;
 };
 
@@ -186,7 +190,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
     const int blk2 = (lane >> 4) & 1;
 
     const int kvh = blockIdx.x % a.Hkv;
-    const int pair = blockIdx.x / a.Hkv;
+    const int pair = blockIdx.x / a.Hkv;   // pair index (paired) or block rank, longest first
     const int b = blockIdx.y;
     const int S = a.S;
     const int G = a.G;
@@ -262,8 +266,14 @@ prefill_mfma_kernel(const PrefillArgs a) {
         // the other half run tile loops (every workgroup of a KV head still
         // walks the same tiles together).
         const bool flip = KG == 2 && (kvh & 1) != 0;
-        const int qblk = (pass == 0) != flip ? pair : a.n_qblk - 1 - pair;
-        if (pass == 1 && a.n_qblk - 1 - pair <= pair) break;   // odd count: middle block once
+        int qblk;
+        if (a.paired) {
+            qblk = (pass == 0) != flip ? pair : a.n_qblk - 1 - pair;
+            if (pass == 1 && a.n_qblk - 1 - pair <= pair) break;   // odd count: middle block once
+        } else {
+            if (pass == 1) break;
+            qblk = a.n_qblk - 1 - pair;   // one block per workgroup, longest first
+        }
         const int q0 = qblk * BM;
 
         // ---- this wave's unit: head kvh*G + u%G, rows r0 .. r0+31; its key
@@ -761,6 +771,7 @@ int prefill_impl(const void* q, const void* k, const void* v, void* out, int64_t
     a.scale_log2 = 1.4426950408889634f / std::sqrt(static_cast<float>(d));
     a.RB = 1;
     a.n_qblk = 0;
+    a.paired = 1;
 
     const bool fast = (d == 64 || d == 128) && a.G <= 8 && aligned16(q) && aligned16(k) &&
                       aligned16(v) && aligned16(out) &&
@@ -777,7 +788,10 @@ int prefill_impl(const void* q, const void* k, const void* v, void* out, int64_t
         a.RB = 8 / kg / a.G;
         const int bm = 32 * a.RB;
         a.n_qblk = static_cast<int>((seq_len + bm - 1) / bm);
-        dim3 grid(hkv * ((a.n_qblk + 1) / 2), batch);
+        // pair the causal blocks only when the pairs fill every CU
+        const int64_t pgrid = (int64_t)hkv * ((a.n_qblk + 1) / 2) * batch;
+        a.paired = (pgrid >= kNumCUs) ? 1 : 0;
+        dim3 grid(hkv * (a.paired ? (a.n_qblk + 1) / 2 : a.n_qblk), batch);
         const dim3 blk(8 * kWave);
         if (d == 64 && kg == 2)
             hipLaunchKernelGGL((prefill_mfma_kernel<64, 2>), grid, blk, 0, s, a);
