@@ -242,14 +242,24 @@ def cpu_baseline_config3(c, torch):
     b, hq, hkv, d = c["b"], c["hq"], c["hkv"], c["d"]
     L1 = c["lens"] + 1
     cap = int(L1.max())
-    kv_k = torch.empty((b, hkv, cap, d), dtype=torch.float16, device="cuda")
-    kv_v = torch.empty_like(kv_k)
-    import kvhp
-    kvhp.paged_gather_kv(c["pool_k"], c["pool_v"], c["bt"], c["lens1"], cap, kv_k, kv_v)
-    torch.cuda.synchronize()
-    kf = kv_k.float().cpu().numpy()
-    vf = kv_v.float().cpu().numpy()
-    del kv_k, kv_v
+    # The oracle's inputs are gathered on the host from the pool and the page
+    # tables (not by the GPU gather under test), with each sequence's new
+    # row at position L_b taken from the step's own new K/V (not from the
+    # GPU's fused append).
+    bt = c["bt_np"]
+    slot = np.arange(cap) % 16
+    page = np.arange(cap) // 16
+    kf = np.zeros((b, hkv, cap, d), np.float32)
+    vf = np.zeros((b, hkv, cap, d), np.float32)
+    new_k = c["new_k"].float().cpu().numpy().reshape(b, hkv, d)
+    new_v = c["new_v"].float().cpu().numpy().reshape(b, hkv, d)
+    for name, dst, new in (("pool_k", kf, new_k), ("pool_v", vf, new_v)):
+        pool = c[name].cpu().numpy()   # [hkv][P][16][d] fp16
+        for i in range(b):
+            n = int(c["lens"][i])
+            dst[i, :, :n, :] = pool[:, bt[i, page[:n]], slot[:n], :]
+            dst[i, :, n, :] = new[i]
+        del pool
     qf = c["q"].float().cpu().numpy()
     threads = min(16, os.cpu_count() or 1)
     nbytes = decode_bytes(L1, hq, hkv, d)
