@@ -65,6 +65,25 @@ def test_decode_d128_splits(L, splits):
     assert_attn_close(got, ref, f"L={L} splits={splits}")
 
 
+@pytest.mark.parametrize("d,L,splits", [(64, 1, 1), (64, 40, 1), (64, 96, 1), (64, 160, 1),
+                                         (64, 224, 2), (64, 700, 3), (128, 33, 1), (128, 129, 1),
+                                         (128, 515, 0)])
+def test_decode_four_wave_splits(d, L, splits):
+    """Fixed-chunk splits run four waves that take the split's 32-token steps
+    round robin and fold their (m, l, O) in LDS: splits of 1..7 steps (waves
+    with no step among them), D=64 multi-split and D=128 single splits."""
+    rng = np.random.default_rng(3000 + 7 * L + d)
+    hq, hkv = 32, 4 if d == 64 else 8
+    q = oracle.normal_f16(rng, (1, hq, d))
+    kc, vc = oracle.normal_f16(rng, (1, hkv, L, d)), oracle.normal_f16(rng, (1, hkv, L, d))
+    note(f"decode four-wave d={d} L={L} splits={splits}")
+    got = _run_contig(q, kc, vc, [L], hq, hkv, d, L, splits)
+    ref = oracle.decode_attention(q.astype(np.float32), kc.astype(np.float32),
+                                  vc.astype(np.float32), np.array([L], np.int32), hq, hkv, d,
+                                  nthreads=8)
+    assert_attn_close(got, ref, f"d={d} L={L} splits={splits}")
+
+
 def test_config1_append_then_decode():
     """B=1, 32/8 heads, D=64, 511 cached tokens, append one
     K/V row at position 511 with the append kernel, then decode over 512."""
