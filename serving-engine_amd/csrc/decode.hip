@@ -148,7 +148,9 @@ __device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
     return __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// One 64-lane workgroup per (split, kv_head, sequence).  Both contractions
+// One workgroup of W waves per (split, kv_head, sequence); wave w takes the
+// split's 32-token steps w, w+W, ... and the waves' states meet in LDS at
+// the end (W = 1: the wave's state is the split's).  Both contractions
 // are transposed so that lane (g, col) -- g = lane/16, col = lane%16 -- owns
 // query head `col` of the KV head's group for the whole online softmax:
 //   S^T = K Q^T   A = K rows of one 16-token page from k_lds (lane: token
@@ -161,7 +163,7 @@ __device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
 //                 16db+col, tokens 4g..4g+3 and 16+4g..16+4g+3), B = P^T in
 //                 fp16 straight from the S^T accumulators (k-slot (g, e) is
 //                 token 4g+e of page 0 for e < 4, of page 1 for e >= 4).
-// K runs two steps ahead in registers, V one step; both are loaded as whole
+// K runs two of the wave's steps ahead in registers, V one; both are loaded as whole
 // rows and staged through LDS (K for the A layout, V for the transposed
 // reads).
 template <int D, int G, bool PAGED, int W>
