@@ -34,8 +34,10 @@
 // eight per CU.
 //
 // Splits: a sequence whose keys fit one split gets its output written
-// directly; otherwise each split stores (m, l, o[D]) in fp32 and
-// decode_merge_kernel (a second, small launch) combines them by log-sum-exp.
+// directly; otherwise each split stores (m, l, o[D]) in fp32 and a second,
+// small launch combines them by log-sum-exp: decode_merge_kernel per (kv
+// head, sequence), or decode_merge_rows_kernel per (query head, sequence)
+// for fixed chunks with 64 KB or more of partials per kv head.
 // An explicit split count cuts every sequence into chunks of one size (grid
 // = split x kv head x sequence).  The automatic count for a batch of 8 or
 // more balances on the device: every workgroup sums the batch's lengths,
@@ -663,6 +665,118 @@ decode_merge_kernel(const DecodeArgs a) {
     }
 }
 
+// Merge for fixed chunks, one workgroup per (query head, sequence), so a
+// small batch spreads its partials over B*Hq CUs instead of B*Hkv (at B=1,
+// D=128, 64 splits, one workgroup per KV head pulls 133 KB through one CU).
+// Lane (r, c): c = lane % LPR owns dims 8c..8c+7, r = lane / LPR is one of
+// R split subsets; wave w's subset r takes splits (w*R + r) + k*W*R.  Every
+// slot of the plan is loaded together with the length (no dependent round
+// trip); slots past the sequence's last split are dropped by selects (their
+// contents may be stale).  The subsets fold by lane exchanges, the waves
+// through LDS.
+template <int D>
+__global__ void __launch_bounds__(kMergeWaves * kWave)
+decode_merge_rows_kernel(const DecodeArgs a) {
+    constexpr int LPR = D / 8;
+    constexpr int R = kWave / LPR;
+    constexpr int STRIDE = kMergeWaves * R;
+    constexpr int U = 4;   // splits per lane per round
+    __shared__ __attribute__((aligned(16))) float red[kMergeWaves - 1][LPR][12];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane % LPR;
+    const int r = lane / LPR;
+    const int b = blockIdx.y;
+    const int64_t row = (int64_t)b * a.Hq + blockIdx.x;
+    const int Lraw = seq_len_of(a, b);
+    const float* po = a.ws_o + row * a.nsplit * D + 8 * c;
+    const float* pml = a.ws_ml + row * a.nsplit * 2;
+
+    float M = -3.0e38f, Sm = 0.f;
+    floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    int nsb = 0;
+    for (int k = 0; k * STRIDE * U < a.nsplit; ++k) {   // uniform over the workgroup
+        const int j0 = k * STRIDE * U + wave * R + r;
+        float2 ml[U];
+        floatx4 x[U][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = min(j0 + STRIDE * u, a.nsplit - 1);
+            ml[u] = *reinterpret_cast<const float2*>(pml + 2 * j);
+            x[u][0] = *reinterpret_cast<const floatx4*>(po + (int64_t)j * D);
+            x[u][1] = *reinterpret_cast<const floatx4*>(po + (int64_t)j * D + 4);
+        }
+        if (k == 0) {   // first round: the length arrives with the loads
+            const int L = min(Lraw, a.cap);
+            if (L <= 0) return;
+            nsb = (L + a.chunk - 1) / a.chunk;
+            if (nsb <= 1) return;   // written directly by the split kernel
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool ok = j0 + STRIDE * u < nsb;
+            const float mu = ok ? ml[u].x : -3.0e38f;
+            const float lu = ok ? ml[u].y : 0.f;
+            const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+            const float mn = fmaxf(M, mu);
+            const float al = fast_exp2(M - mn);
+            const float be = fast_exp2(mu - mn);
+            acc0 = acc0 * al + (ok ? x[u][0] : z) * be;
+            acc1 = acc1 * al + (ok ? x[u][1] : z) * be;
+            Sm = fmaf(Sm, al, lu * be);
+            M = mn;
+        }
+    }
+    // fold the R subsets of the wave (lanes c, c + LPR, ...)
+#pragma unroll
+    for (int o = LPR; o < kWave; o <<= 1) {
+        const float mo = __shfl_xor(M, o);
+        const float so = __shfl_xor(Sm, o);
+        floatx4 x0, x1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x0[e] = __shfl_xor(acc0[e], o);
+            x1[e] = __shfl_xor(acc1[e], o);
+        }
+        const float mn = fmaxf(M, mo);
+        const float al = fast_exp2(M - mn);
+        const float be = fast_exp2(mo - mn);
+        acc0 = acc0 * al + x0 * be;
+        acc1 = acc1 * al + x1 * be;
+        Sm = Sm * al + so * be;
+        M = mn;
+    }
+    if (wave > 0 && r == 0) {
+        float* p = red[wave - 1][c];
+        *reinterpret_cast<floatx4*>(p) = acc0;
+        *reinterpret_cast<floatx4*>(p + 4) = acc1;
+        p[8] = M;
+        p[9] = Sm;
+    }
+    __syncthreads();
+    if (wave != 0 || r != 0) return;
+#pragma unroll
+    for (int w = 0; w < kMergeWaves - 1; ++w) {
+        const float* p = red[w][c];
+        const float mn = fmaxf(M, p[8]);
+        const float al = fast_exp2(M - mn);
+        const float be = fast_exp2(p[8] - mn);
+        acc0 = acc0 * al + *reinterpret_cast<const floatx4*>(p) * be;
+        acc1 = acc1 * al + *reinterpret_cast<const floatx4*>(p + 4) * be;
+        Sm = Sm * al + p[9] * be;
+        M = mn;
+    }
+    const float inv = Sm > 0.f ? 1.f / Sm : 0.f;
+    half8 hv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        hv[e] = static_cast<f16>(acc0[e] * inv);
+        hv[4 + e] = static_cast<f16>(acc1[e] * inv);
+    }
+    store_half8(a.out + row * D + 8 * c, hv);
+}
+
 // Any head_dim <= 256, any group size, any page size, any strides: one wave
 // per (q_head, sequence), one pass over the keys with an online softmax.
 // Serves shapes outside the fast kernel's template set.
@@ -916,7 +1030,15 @@ void launch_fast(const DecodeArgs& args, dim3 grid, bool paged, hipStream_t s) {
         else
             hipLaunchKernelGGL((decode_splitk_kernel<D, G, false, 1>), grid, dim3(kWave), 0, s, a);
     }
-    if (a.nsplit > 1)
+    // fixed chunks with >= 64 KB of partials per (kv head, sequence): one
+    // merge workgroup per query head (config 2 at 64K: 50.2 vs 51.2 us;
+    // below that, e.g. config 5's 38 KB, the per-kv-head merge is faster)
+    const bool rows_merge =
+        a.balance <= 0 && (long long)a.nsplit * G * (D + 2) * sizeof(float) >= (64 << 10);
+    if (a.nsplit > 1 && rows_merge)
+        hipLaunchKernelGGL((decode_merge_rows_kernel<D>), dim3(a.Hq, a.batch),
+                           dim3(kMergeWaves * kWave), 0, s, a);
+    else if (a.nsplit > 1)
         hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.Hkv, a.batch),
                            dim3(kMergeWaves * kWave), 0, s, a);
 }

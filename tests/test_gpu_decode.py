@@ -365,20 +365,22 @@ def test_decode_caller_workspace_reuse_and_empty_sequences():
         assert np.all(got[np.array(lens) == 0] == 0)
 
 
-@pytest.mark.parametrize("balanced", [False, True])
-def test_decode_ignores_stale_workspace_slots(balanced):
+@pytest.mark.parametrize("balanced,d,fixed_splits", [(False, 128, 32), (False, 64, 64),
+                                                      (True, 128, 0)])
+def test_decode_ignores_stale_workspace_slots(balanced, d, fixed_splits):
     """The merge reads every split slot of a sequence before it knows how
     many the sequence used; slots it did not use may hold anything.  A
     caller workspace filled with NaN bytes (and one filled with huge values)
-    must not change a single output: short sequences use few of the 32
+    must not change a single output: short sequences use few of the
     slots, one uses many.  Balanced: a batch of 12 in the automatic split
-    mode; otherwise an explicit 32-way split."""
+    mode; otherwise an explicit 32- or 64-way split (both take the
+    per-query-head merge: >= 64 KB of partials per kv head)."""
     import torch
-    rng = np.random.default_rng(77 + balanced)
-    hq, hkv, d, cap = 32, 8, 128, 4096
+    rng = np.random.default_rng(77 + balanced + d)
+    hq, hkv, cap = 32, 8, 4096
     lens = [4096, 40, 1, 300, 0, 2000] * (2 if balanced else 1)
     b = len(lens)
-    splits = 0 if balanced else 32
+    splits = fixed_splits
     ws_bytes = kvhp.decode_workspace_bytes(b, hq, hkv, d, cap, splits)
     q = oracle.normal_f16(rng, (b, hq, d))
     kc, vc = oracle.normal_f16(rng, (b, hkv, cap, d)), oracle.normal_f16(rng, (b, hkv, cap, d))
@@ -387,7 +389,7 @@ def test_decode_ignores_stale_workspace_slots(balanced):
     outs = []
     for fill in (0xFF, 0x7F):          # NaN bytes; 3.4e38-ish floats
         ws = torch.full((ws_bytes,), fill, dtype=torch.uint8, device="cuda")
-        note(f"stale workspace fill=0x{fill:02x} balanced={balanced}")
+        note(f"stale workspace fill=0x{fill:02x} balanced={balanced} d={d}")
         got = _run_contig(q, kc, vc, lens, hq, hkv, d, cap, splits, ws)
         assert np.isfinite(got).all(), f"fill 0x{fill:02x}: non-finite output"
         assert_attn_close(got, ref, f"fill 0x{fill:02x}")
