@@ -465,7 +465,9 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
 
     half8 wa[C], wb[C];
     int tile = static_cast<int>(blockIdx.x);
-    if constexpr (kDB) load_w(tile, wa);
+    if constexpr (kSeq) {
+        if constexpr (kDB) load_w(tile, wa);
+    }
 
     // x slice of every batch tile, resident for all tiles (RMSNorm applied)
     half8 xr[kSeq ? 1 : NBT][C];
@@ -477,6 +479,9 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
 #pragma unroll
             for (int t = 0; t < C; ++t) nw[t] = load_half8(a.norm_w + ks + 32 * t);
         }
+        // the first tile's weights after x: the RMSNorm below waits for x
+        // only, the weights keep landing under it
+        if constexpr (kDB) load_w(tile, wa);
         // every load above in flight before the first use (one round trip;
         // the scheduler would otherwise pair loads with their uses)
         __builtin_amdgcn_sched_barrier(0);
