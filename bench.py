@@ -70,13 +70,14 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5,c5b,kv")
     ap.add_argument("--profile", nargs="?", const="decode", default=None,
-                    choices=("decode", "prefill", "c5", "batched"),
+                    choices=("decode", "prefill", "c5", "batched", "c2"),
                     help="short run for rocprofv3: a 256 MiB device copy (counter "
                          "calibration) then the config-3 steps (decode), config-4 "
                          "S=2048 prefill calls (prefill), --steps config-5 decode "
-                         "steps without the HIP graph (c5) or --steps batched decode "
-                         "steps of the config-5 model at B = 1, 8, 32 (batched); no "
-                         "CPU baseline, no extras")
+                         "steps without the HIP graph (c5), --steps batched decode "
+                         "steps of the config-5 model at B = 1, 8, 32 (batched) or "
+                         "--steps flushed config-2 calls (auto splits) per context "
+                         "(c2); no CPU baseline, no extras")
     return ap.parse_args()
 
 
@@ -606,7 +607,7 @@ def run_config1(torch, kvhp):
     return res
 
 
-def run_config2(torch, kvhp, stream_gbps=None):
+def run_config2(torch, kvhp, stream_gbps=None, splits=(1, 4, 16, 64, 0), reps=15):
     hq, hkv, d = 32, 8, 128
     fl = Flusher(torch)
     rows = []
@@ -620,7 +621,7 @@ def run_config2(torch, kvhp, stream_gbps=None):
         kv = kvhp.strided_view(kc, hkv * L * d, L * d, d)
         vv = kvhp.strided_view(vc, hkv * L * d, L * d, d)
         nb = decode_bytes([L], hq, hkv, d)
-        for s in (1, 4, 16, 64, 0):
+        for s in splits:
             ws_b = kvhp.decode_workspace_bytes(1, hq, hkv, d, L, s)
             ws = torch.empty(max(ws_b, 256), dtype=torch.uint8, device="cuda")
             kvhp.decode_workspace_init(ws)
@@ -630,7 +631,7 @@ def run_config2(torch, kvhp, stream_gbps=None):
 
             for _ in range(3):
                 fn()
-            t = time_op(torch, fn, 15, fl)
+            t = time_op(torch, fn, reps, fl)
             row = {"ctx": L, "splits": s if s else f"auto({kvhp.decode_auto_splits(1, hkv, d, L)})",
                    **spread(t, nb), "pct_hbm": round(nb / t[0] / 1e3 / HBM_PEAK_GBS * 100, 1)}
             if stream_gbps:
@@ -895,6 +896,10 @@ def main():
         if args.profile == "c5":
             r5 = run_config5_eager(torch, kvhp, steps=args.steps)
             print(json.dumps({"profile": "c5", "config5": r5}))
+            return
+        if args.profile == "c2":
+            r2 = run_config2(torch, kvhp, splits=(0,), reps=args.steps)
+            print(json.dumps({"profile": "c2", "config2": r2}))
             return
         if args.profile == "batched":
             rb = run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=args.steps)
