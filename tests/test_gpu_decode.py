@@ -175,10 +175,13 @@ def _paged_case(rng, b, lens, hq, hkv, d, with_append, fused=False):
 
 @pytest.mark.parametrize("b,maxlen,hq,hkv,d", [(8, 1500, 32, 8, 128), (5, 300, 14, 2, 64),
                                                (3, 900, 32, 4, 64), (4, 200, 16, 1, 128),
-                                               (80, 3000, 32, 8, 128), (70, 900, 32, 4, 64)])
+                                               (80, 3000, 32, 8, 128), (70, 900, 32, 4, 64),
+                                               (3, 6000, 32, 8, 128)])
 def test_paged_decode_with_append(b, maxlen, hq, hkv, d):
     """Ragged paged batches (lengths from 0); batches of 8 or more run the
-    balanced split list (above 64 sequences its scan takes two passes)."""
+    balanced split list (above 64 sequences its scan takes two passes); a
+    small batch of long sequences takes fixed chunks with >= 64 KB of
+    partials per kv head, merged per query head."""
     rng = np.random.default_rng(b * 31 + maxlen)
     lens = rng.integers(0, maxlen, size=b)
     note(f"paged decode B={b} Hq={hq} Hkv={hkv} D={d} lens={lens.tolist()}")
