@@ -425,7 +425,13 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int NW = static_cast<int>(blockDim.x >> 6);
     const int g = lane >> 4, col = lane & 15;
-    const int ks = w * 32 * C + 8 * g;
+    // Wave w holds K slice (w + rot) % NW: the workgroups of one XCD
+    // (blockIdx.x equal mod 8) start their x loads on different slices
+    // instead of all reading the same lines at once.  Partial sums are
+    // still added in slice order, so results do not depend on rot.
+    const int rot = static_cast<int>((blockIdx.x >> 3) % static_cast<unsigned>(NW));
+    const int sl = w + rot < NW ? w + rot : w + rot - NW;
+    const int ks = sl * 32 * C + 8 * g;
     const int G = static_cast<int>(gridDim.x);
     const int n_my = (a.tiles - static_cast<int>(blockIdx.x) + G - 1) / G;
 
@@ -508,7 +514,7 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
 #pragma unroll
             for (int bt = 0; bt < NBT; ++bt) {
                 float tot = 0.f;
-                for (int i = 0; i < NW; ++i) tot += ssq[bt][i][col];
+                for (int i = 0; i < NW; ++i) tot += ssq[bt][i >= rot ? i - rot : i - rot + NW][col];
                 const float rs = 1.f / sqrtf(tot / static_cast<float>(a.K) + a.eps);
 #pragma unroll
                 for (int t = 0; t < C; ++t)
@@ -540,9 +546,10 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
         const int b = 16 * bt + n;
         if (b >= a.B || m >= (kPair ? P : L)) return;
         float v0 = 0.f, v1 = 0.f;
-        for (int i = 0; i < NW; ++i) {
-            v0 += red[rb][i][bt][m * 16 + n];
-            if constexpr (kPair) v1 += red[rb][i][bt][(m + P) * 16 + n];
+        for (int i = 0; i < NW; ++i) {   // slice i sits in wave (i - rot) mod NW
+            const int wi = i >= rot ? i - rot : i - rot + NW;
+            v0 += red[rb][wi][bt][m * 16 + n];
+            if constexpr (kPair) v1 += red[rb][wi][bt][(m + P) * 16 + n];
         }
         if constexpr (EPI == kEpiQKV) {
             const int tph = a.D / L;
