@@ -277,6 +277,18 @@ int kvhp_rmsnorm_qkv_rope_append(const void* W_qkv, const void* x, const void* n
  * position marks an idle row (q written, nothing appended). */
 int kvhp_gemv_residual_rows(const void* W, const void* x, const void* r, void* y, int N, int K,
                             int batch, void* stream);
+/* No counterpart in the reference (its batched projections are library
+ * GEMMs).  kvhp_gemv_residual_rows with a caller workspace: when the batch's
+ * x exceeds 160 KB (batch*K > 81920, e.g. the down projection, K = 5632,
+ * from 15 rows) and N % 16 == 0, the product is split over K into fp32
+ * partials (kvhp_gemv_rows_workspace_bytes bytes) and summed by a second
+ * launch, so that no CU loads all of x; the output is bit-identical to
+ * kvhp_gemv_residual_rows.  Workspace bytes 0 (or workspace NULL): the
+ * single-launch path.  r may alias y. */
+size_t kvhp_gemv_rows_workspace_bytes(int N, int K, int batch);
+int kvhp_gemv_residual_rows_ws(const void* W, const void* x, const void* r, void* y, int N,
+                               int K, int batch, void* workspace, size_t workspace_bytes,
+                               void* stream);
 int kvhp_rmsnorm_gemv_rows(const void* W, const void* x, const void* norm_w, float eps, void* y16,
                            float* y32, int N, int K, int batch, void* stream);
 int kvhp_rmsnorm_gemv_swiglu_rows(const void* W_gate_up, const void* x, const void* norm_w,

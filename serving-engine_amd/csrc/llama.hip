@@ -88,6 +88,8 @@ struct Model {
     size_t ws_bytes = 0;
     void* ws_rows = nullptr;   // decode attention workspace of the batched paths (grows)
     size_t ws_rows_bytes = 0;
+    void* part_rows = nullptr; // K-split partials of the batched down projection (grows)
+    size_t part_rows_bytes = 0;
     int prompt_len = 0;
     bool rows_ok = false;      // batched projections fit the skinny-GEMM kernels
     hipGraph_t graph = nullptr;
@@ -392,7 +394,15 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
     }
     if (B <= 32 && m.rows_ok) {
         // Skinny-GEMM projections with the batch-1 step's fusions: every
-        // weight read once per step for all B rows, six launches per layer.
+        // weight read once per step for all B rows, six launches per layer
+        // (seven when the down projection's x is large enough to split over
+        // K: its partials live in the model's own buffer).
+        const size_t part_need = kvhp_gemv_rows_workspace_bytes(H, F, B);
+        if (part_need > m.part_rows_bytes) {
+            char* p = static_cast<char*>(m.part_rows);
+            KVHP_TRY(regrow(m, &p, &m.part_rows_bytes, part_need, static_cast<hipStream_t>(s)));
+            m.part_rows = p;
+        }
         for (int l = 0; l < c.num_layers; ++l) {
             const Layer& L = m.layers[l];
             KVHP_TRY(kvhp_rmsnorm_qkv_rope_append_rows(
@@ -405,7 +415,8 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
             KVHP_TRY(kvhp_gemv_residual_rows(L.w_o, m.attn, m.hidden, m.hidden, H, Hq * D, B, s));
             KVHP_TRY(kvhp_rmsnorm_gemv_swiglu_rows(L.w_gate_up, m.hidden, L.ffn_norm, c.rms_eps,
                                                    m.act, F, H, B, s));
-            KVHP_TRY(kvhp_gemv_residual_rows(L.w_down, m.act, m.hidden, m.hidden, H, F, B, s));
+            KVHP_TRY(kvhp_gemv_residual_rows_ws(L.w_down, m.act, m.hidden, m.hidden, H, F, B,
+                                                part_need ? m.part_rows : nullptr, part_need, s));
         }
         KVHP_TRY(kvhp_rmsnorm_gemv_rows(m.lm_head, m.hidden, m.final_norm, c.rms_eps, nullptr,
                                         logits, c.vocab_size, H, B, s));

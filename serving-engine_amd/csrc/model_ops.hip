@@ -746,6 +746,117 @@ int launch_rows(RowsArgs a, hipStream_t s, const char* what) {
     return check_launch(what);
 }
 
+// ---- Batched residual projection split over K (large B*K) ---------------------
+// Every workgroup of gemm_rows_kernel loads all B rows of x, B*K*2 bytes per
+// CU (360 KB for the down projection at B = 32, more than its weights).
+// Split over K instead: workgroup (row group, slice) stages the B x 32C slice
+// of x in LDS once (22.5 KB at B = 32, C = 11) and its kWpg waves each
+// multiply one 16-row weight tile by it, writing fp32 partial sums
+// part[slice][b][n]; a second launch adds the slices in order and the
+// residual.  The slices are gemm_rows_kernel's per-wave K slices and both
+// sum them in slice order, so the result is bit-identical to it.
+constexpr int kWpg = 8;        // weight tiles (waves) per workgroup
+constexpr int kMaxSlices = 16;
+
+template <int C, int NBT>
+__global__ void __launch_bounds__(kWave * kWpg) ksplit_partial_kernel(const RowsArgs a,
+                                                                      float* part) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g = lane >> 4, col = lane & 15;
+    const int slice = static_cast<int>(blockIdx.y);
+    const int k0 = slice * 32 * C;
+    const int tile = static_cast<int>(blockIdx.x) * kWpg + w;
+    __shared__ half8 xs[NBT][16][C][4];   // [batch tile][batch row][chunk t][k group g]
+
+    // this wave's weight tile first (streamed once; rows past N repeat row N-1)
+    half8 wr[C];
+    const int row = min(tile * 16 + col, a.N - 1);
+    const f16* wp = a.W + (int64_t)row * a.K + k0 + 8 * g;
+#pragma unroll
+    for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(wp + 32 * t);
+    // x slice of every batch row, zero past B
+    for (int i = static_cast<int>(threadIdx.x); i < NBT * 16 * 4 * C; i += kWave * kWpg) {
+        const int r = i / (4 * C), ch = i % (4 * C);   // ch = 4t + k group
+        half8 v = {};
+        if (r < a.B) v = load_half8(a.x + (int64_t)r * a.K + k0 + 8 * ch);
+        xs[r / 16][r % 16][ch / 4][ch % 4] = v;
+    }
+    __syncthreads();
+    floatx4 acc[NBT];
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) {
+        acc[bt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < C; ++t)
+            acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wr[t], xs[bt][col][t][g], acc[bt], 0,
+                                                             0, 0);
+    }
+    // lane (g, col): rows 4g..4g+3 of the tile for batch row col of each batch tile
+    const int n0 = tile * 16 + 4 * g;
+    if (n0 >= a.N) return;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) {
+        const int b = 16 * bt + col;
+        if (b < a.B)
+            *reinterpret_cast<floatx4*>(part + ((int64_t)slice * a.B + b) * a.N + n0) = acc[bt];
+    }
+}
+
+// y[b][n] = fp16(sum over slices in order + resid[b][n]); 4 outputs per thread
+// (resid may alias y: each element is read and written by one thread).
+__global__ void __launch_bounds__(128) ksplit_reduce_residual_kernel(const RowsArgs a,
+                                                                     const float* part,
+                                                                     int slices) {
+    const int64_t i = (int64_t)blockIdx.x * 128 + threadIdx.x;
+    const int64_t total = (int64_t)a.B * a.N;
+    if (i * 4 >= total) return;
+    const int64_t o = i * 4;
+    floatx4 p[kMaxSlices];
+#pragma unroll
+    for (int s = 0; s < kMaxSlices; ++s)
+        p[s] = s < slices ? *reinterpret_cast<const floatx4*>(part + s * total + o)
+                          : floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kMaxSlices; ++s)
+        if (s < slices) v += p[s];
+    const int64_t b = o / a.N, n = o % a.N;   // N % 16 == 0: the 4 outputs share a row
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int64_t yo = b * a.ldy + n + e;
+        a.y16[yo] = static_cast<f16>(v[e] + static_cast<float>(a.resid[yo]));
+    }
+}
+
+// Bytes of fp32 partials the K-split path needs for this call, 0 when the
+// call keeps gemm_rows_kernel: batches whose x exceeds 160 KB per CU
+// (B*K > 81920: the down projection, K = 5632, from B = 15), N % 16 == 0.
+size_t ksplit_bytes(int N, int K, int B) {
+    int C = 0, NW = 0;
+    if (B < 1 || B > 32 || N % 16 != 0 || !rows_shape(K, C, NW)) return 0;
+    if ((int64_t)B * K <= 81920) return 0;
+    return sizeof(float) * (size_t)NW * B * N;
+}
+
+int launch_ksplit_residual(const RowsArgs& a, float* part, hipStream_t s, const char* what) {
+    int C = 0, NW = 0;
+    rows_shape(a.K, C, NW);
+    const dim3 grid((a.N / 16 + kWpg - 1) / kWpg, NW);
+    const dim3 blk(kWave * kWpg);
+    if (C == 8 && a.B <= 16)
+        hipLaunchKernelGGL((ksplit_partial_kernel<8, 1>), grid, blk, 0, s, a, part);
+    else if (C == 8)
+        hipLaunchKernelGGL((ksplit_partial_kernel<8, 2>), grid, blk, 0, s, a, part);
+    else if (a.B <= 16)
+        hipLaunchKernelGGL((ksplit_partial_kernel<11, 1>), grid, blk, 0, s, a, part);
+    else
+        hipLaunchKernelGGL((ksplit_partial_kernel<11, 2>), grid, blk, 0, s, a, part);
+    const int64_t threads = (int64_t)a.B * a.N / 4;
+    hipLaunchKernelGGL(ksplit_reduce_residual_kernel, dim3((unsigned)((threads + 127) / 128)),
+                       dim3(128), 0, s, a, part, NW);
+    return check_launch(what);
+}
+
 // Row-wise RMSNorm (prefill): one workgroup of 256 threads per row.
 __global__ void __launch_bounds__(256)
 rmsnorm_rows_kernel(const f16* x, const f16* w, f16* out, int dim, float eps) {
@@ -1121,6 +1232,39 @@ extern "C" int kvhp_gemv_residual_rows(const void* W, const void* x, const void*
     a.ldy = N;
     return launch_rows<kEpiResidual, false>(a, static_cast<hipStream_t>(stream),
                                                "gemv_residual_rows");
+}
+
+extern "C" size_t kvhp_gemv_rows_workspace_bytes(int N, int K, int batch) {
+    return ksplit_bytes(N, K, batch);
+}
+
+extern "C" int kvhp_gemv_residual_rows_ws(const void* W, const void* x, const void* r, void* y,
+                                          int N, int K, int batch, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+    clear_error();
+    if (N == 0 || batch == 0) return KVHP_OK;
+    const size_t need = ksplit_bytes(N, K, batch);
+    if (need == 0 || workspace == nullptr)
+        return kvhp_gemv_residual_rows(W, x, r, y, N, K, batch, stream);
+    int rc = check_gemv(W, x, N, K, "gemv_residual_rows_ws");
+    if (rc) return rc;
+    KVHP_REQUIRE(r && y, KVHP_ERR_INVALID, "gemv_residual_rows_ws: null residual/output");
+    KVHP_REQUIRE(workspace_bytes >= need, KVHP_ERR_WORKSPACE,
+                 "gemv_residual_rows_ws: workspace of %zu bytes, this call needs %zu",
+                 workspace_bytes, need);
+    KVHP_REQUIRE(aligned16(W) && aligned16(x) && aligned16(workspace), KVHP_ERR_UNSUPPORTED,
+                 "gemv_residual_rows_ws: W, x and the workspace must be 16-byte aligned");
+    RowsArgs a{};
+    a.W = static_cast<const f16*>(W);
+    a.x = static_cast<const f16*>(x);
+    a.N = N;
+    a.K = K;
+    a.B = batch;
+    a.resid = static_cast<const f16*>(r);
+    a.y16 = static_cast<f16*>(y);
+    a.ldy = N;
+    return launch_ksplit_residual(a, static_cast<float*>(workspace),
+                                  static_cast<hipStream_t>(stream), "gemv_residual_rows_ws");
 }
 
 extern "C" int kvhp_rmsnorm_gemv_rows(const void* W, const void* x, const void* norm_w, float eps,

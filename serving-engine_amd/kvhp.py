@@ -93,6 +93,8 @@ _SIGNATURES = {
     "kvhp_rmsnorm_qkv_rope_append": (_i32, [_vp, _vp, _vp, _f32, _vp, _f32, _vp, _vp, _vp, _vp,
                                             _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "kvhp_gemv_residual_rows": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "kvhp_gemv_rows_workspace_bytes": (_sz, [_i32, _i32, _i32]),
+    "kvhp_gemv_residual_rows_ws": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _sz, _vp]),
     "kvhp_rmsnorm_gemv_rows": (_i32, [_vp, _vp, _vp, _f32, _vp, _vp, _i32, _i32, _i32, _vp]),
     "kvhp_rmsnorm_gemv_swiglu_rows": (_i32, [_vp, _vp, _vp, _f32, _vp, _i32, _i32, _i32, _vp]),
     "kvhp_rmsnorm_qkv_rope_append_rows": (_i32, [_vp, _vp, _vp, _f32, _vp, _f32, _vp, _vp, _vp,
@@ -370,6 +372,18 @@ def rmsnorm_qkv_rope_append(W_qkv, x, norm_w, eps, seq_len, theta, q_out, pool_k
 def gemv_residual_rows(W, x, r, y, N, K, batch, stream=None):
     _check(load().kvhp_gemv_residual_rows(_ptr(W), _ptr(x), _ptr(r), _ptr(y), N, K, batch,
                                           _stream(stream)))
+
+
+def gemv_rows_workspace_bytes(N, K, batch):
+    return load().kvhp_gemv_rows_workspace_bytes(N, K, batch)
+
+
+def gemv_residual_rows_ws(W, x, r, y, N, K, batch, workspace=None, stream=None):
+    """gemv_residual_rows with a caller workspace (uint8 tensor): large
+    batches split over K; bit-identical output."""
+    nbytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(load().kvhp_gemv_residual_rows_ws(_ptr(W), _ptr(x), _ptr(r), _ptr(y), N, K, batch,
+                                             _ptr(workspace), nbytes, _stream(stream)))
 
 
 def rmsnorm_gemv_rows(W, x, norm_w, eps, N, K, batch, y16=None, y32=None, stream=None):

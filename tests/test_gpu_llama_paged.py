@@ -37,8 +37,8 @@ torch = pytest.importorskip("torch")
 PAGE = 16
 
 
-def _cfg():
-    return kvhp.LlamaConfig(2048, 512, 3, 8, 2, 64, 1024, 1e-5, 10000.0, 0)
+def _cfg(ffn=1024):
+    return kvhp.LlamaConfig(2048, 512, 3, 8, 2, 64, ffn, 1e-5, 10000.0, 0)
 
 
 def _weights(model, cfg):
@@ -167,13 +167,16 @@ def test_paged_runner_matches_batch1_runner_and_oracle():
     model.close()
 
 
-def test_paged_runner_large_batch_path_matches_fused_path():
+@pytest.mark.parametrize("ffn", [1024, 5632])
+def test_paged_runner_large_batch_path_matches_fused_path(ffn):
     """Batches above 32 run on library GEMMs with separate norm / RoPE /
     SwiGLU launches; up to 32 on the fused batched projections.  One step
     of 40 sequences on one copy of the pool against the same step as two
     calls of 20 on another copy: logits within 2% of the scale, tokens equal
-    outside near-ties, and the appended K/V rows within fp16 rounding."""
-    cfg = _cfg()
+    outside near-ties, and the appended K/V rows within fp16 rounding.  With
+    the config-5 FFN width (5632) the calls of 20 split the down projection
+    over K (kvhp_gemv_residual_rows_ws with the model's own partials)."""
+    cfg = _cfg(ffn)
     L, Hkv, D, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
     B, plen, max_pages = 40, 9, 2
     P = B * max_pages

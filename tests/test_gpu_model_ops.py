@@ -152,6 +152,40 @@ def test_gemv_residual_rows(batch, n, k):
     _close(_cpu(y), _f16(ref + r.astype(np.float32)), f"gemv_residual_rows B={batch} {n}x{k}")
 
 
+@pytest.mark.parametrize("batch,n,k", [(15, 2048, 5632), (16, 2048, 5632), (32, 2048, 5632),
+                                       (24, 144, 5632), (32, 4096, 2816), (21, 2048, 4224),
+                                       (32, 2048, 2048), (17, 2040, 5632)])
+def test_gemv_residual_rows_ksplit(batch, n, k):
+    """The workspace form splits large batches over K (partials summed in
+    slice order by a second launch): its output is bit-identical to the
+    single-launch kernel's, in place like the model calls it, and within the
+    oracle tolerance.  Shapes with B*K <= 81920 or N % 16 != 0 need no
+    workspace and take the single launch."""
+    rng = np.random.default_rng(batch * 7 + n + k)
+    W = oracle.normal_f16(rng, (n, k), 0.02)
+    x = oracle.normal_f16(rng, (batch, k))
+    r = oracle.normal_f16(rng, (batch, n))
+    need = kvhp.gemv_rows_workspace_bytes(n, k, batch)
+    splits = k // 256 if k % 256 == 0 and k // 256 <= 8 else k // 352   # the per-wave K slices
+    if batch * k > 81920 and n % 16 == 0:
+        assert need == 4 * splits * batch * n
+    else:
+        assert need == 0
+    Wg, xg = to_gpu(W), to_gpu(x)
+    y1 = to_gpu(r)
+    kvhp.gemv_residual_rows(Wg, xg, y1, y1, n, k, batch)
+    ws = torch.full((max(need, 16),), 0xFF, dtype=torch.uint8, device="cuda")   # NaN bytes
+    y2 = to_gpu(r)
+    kvhp.gemv_residual_rows_ws(Wg, xg, y2, y2, n, k, batch, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2), f"B={batch} {n}x{k}: K-split output differs from the single launch"
+    ref = oracle.matmul_transB(x.astype(np.float32), W.astype(np.float32), nthreads=8)
+    _close(_cpu(y2), _f16(ref + r.astype(np.float32)), f"gemv_residual_rows_ws B={batch} {n}x{k}")
+    if need:
+        with pytest.raises(kvhp.KVHPError):                 # workspace too small
+            kvhp.gemv_residual_rows_ws(Wg, xg, y2, y2, n, k, batch, ws[:need - 16])
+
+
 @pytest.mark.parametrize("batch", ROWS_BATCHES)
 @pytest.mark.parametrize("n,k", [(32000, 2048), (2048, 2048), (77, 512)])
 def test_rmsnorm_gemv_rows(batch, n, k):
