@@ -63,6 +63,20 @@ def test_workspace_sizing():
         assert n == used * b * hq * (d + 2) * 4
 
 
+def test_rows_ksplit_workspace_sizing():
+    # the residual projection splits over K only when the batch's x passes
+    # 160 KB (B*K > 81920) and N % 16 == 0: the down projection (K = 5632,
+    # 16 slices of 352) from 15 rows; fp32 partials slices * B * N
+    size = kvhp.gemv_rows_workspace_bytes
+    assert size(2048, 5632, 14) == 0
+    assert size(2048, 5632, 15) == 16 * 15 * 2048 * 4
+    assert size(2048, 5632, 32) == 16 * 32 * 2048 * 4
+    assert size(4096, 2816, 32) == 8 * 32 * 4096 * 4     # 8 slices of 352
+    assert size(2048, 2048, 32) == 0                      # x of 128 KB: one launch
+    assert size(2040, 5632, 32) == 0                      # N not a multiple of 16
+    assert size(2048, 5632, 33) == 0 and size(2048, 1000, 32) == 0   # unsupported shapes
+
+
 def _null_view():
     return kvhp.KVView()
 
