@@ -362,7 +362,11 @@ prefill_mfma_kernel(const PrefillArgs a) {
             // Operand reads run PF reads ahead of the MFMAs that use them.
             constexpr int NQK = NKB * NC, NPV = 2 * NKB * NDB;   // MFMAs
             constexpr int PF = 8;
+            // The MFMA step runs at wave priority 1: when the SIMD's other wave
+            // (softmax step) and this one both can issue, the MFMAs go first
+            // (S=8192 516 vs 524 us; the key-split loop gains nothing from it).
             auto mstep = [&](int j) {   // 1 <= j < n_tiles
+                __builtin_amdgcn_s_setprio(1);
                 qk(ring + (j % NSTAGE) * 2 * TB, sc);
                 pv(j - 1);
                 __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
@@ -377,6 +381,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
                     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
                 }
                 __builtin_amdgcn_sched_group_barrier(0x008, NQK + NPV - (NQK - PF) - NPV, 0);
+                __builtin_amdgcn_s_setprio(0);
             };
             auto sstep = [&](int j) {
                 const int k0 = j * kBN;
