@@ -15,17 +15,16 @@
 // head fastest.
 //
 // K/V staging: a 4-stage LDS ring (4 x 32 KB for D=128), filled by
-// global_load_lds_dwordx4 (direct HBM->LDS, no VGPR round trip).  Tile t+3 is
-// issued while tile t is consumed; before reading a stage each wave waits for
-// its own loads of that stage (explicit s_waitcnt vmcnt(N)) and the
-// workgroup meets at one barrier per tile.  Rows are stored with an XOR
+// global_load_lds_dwordx4 (direct HBM->LDS, no VGPR round trip).  Tile t+2 is
+// issued when tile t's phases begin; before reading a stage each wave waits
+// for its own loads of that stage (explicit s_waitcnt vmcnt(N)) and the
+// workgroup meets at one barrier per ping-pong phase.  Rows are stored with an XOR
 // swizzle of their 16-byte chunks so that both the K reads (ds_read_b128)
 // and the transposing V reads (ds_read_b64_tr_b16) are bank-conflict free.
 //
 // Per tile and unit, on v_mfma_f32_32x32x16_f16, transposed so that one lane
 // owns one query row for the whole online softmax:
-//   S^T = K Q^T     A = K rows from LDS, B = Q^T held in registers; the S^T of
-//                   tile t+1 is computed before the softmax of tile t.
+//   S^T = K Q^T     A = K rows from LDS, B = Q^T held in registers.
 //   softmax         fp32 in the log2 domain; the causal mask is applied only on
 //                   tiles that cross the diagonal; the running max moves (and
 //                   O is rescaled) only when a row's max passes it by 8 in
@@ -34,9 +33,9 @@
 //   O^T += V^T P^T  A = V^T read with ds_read_b64_tr_b16 (transposing 8-byte
 //                   LDS reads), B = P^T converted to fp16 straight from the
 //                   S^T accumulators.
-// Long prompts (one unit per wave) run the tile loop as a ping-pong instead:
-// waves 0-3 and 4-7 alternate an MFMA step (S^T of tile j, O^T of tile j-1,
-// operand reads scheduled ahead) and a softmax step one phase apart.
+// The tile loop is a ping-pong: waves 0-3 and 4-7 (one of each per SIMD)
+// alternate an MFMA step (S^T of tile j, O^T of tile j-1, operand reads
+// scheduled ahead, at wave priority 1) and a softmax step one phase apart.
 //
 // With a page pool, each workgroup also writes the K/V rows of its own query
 // block into the pages after its outputs (every key row is written exactly
@@ -303,283 +302,175 @@ prefill_mfma_kernel(const PrefillArgs a) {
         const int n_tiles = last_row / kBN + 1;
         last_tile = n_tiles - 1;
 
-        if constexpr (KG == 1) {
-            wait_vmcnt<0>();  // q in registers before the ring: no compiler waits inside it
-            ring_barrier();   // everyone is done with the previous pass's stages
-            issue(ring, 0);
-            issue(ring + 2 * TB, 1);
+        wait_vmcnt<0>();  // q in registers before the ring: no compiler waits inside it
+        ring_barrier();   // everyone is done with the previous pass's stages
+        issue(ring, 0);
+        issue(ring + 2 * TB, 1);
 
-            constexpr int NKB = 2 / KG;     // this wave's 32-key blocks per tile
-            auto qk = [&](const f16* Kt, floatx16 (&sc)[NKB]) {
+        constexpr int NKB = 2 / KG;     // this wave's 32-key blocks per tile
+        auto qk = [&](const f16* Kt, floatx16 (&sc)[NKB]) {
 #pragma unroll
-                for (int kb2 = 0; kb2 < NKB; ++kb2) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) sc[kb2][i] = 0.f;
-#pragma unroll
-                    for (int c = 0; c < NC; ++c) {
-                        const half8 kop = *reinterpret_cast<const half8*>(&Kt[kro[c] + 32 * kb2 * D]);
-                        sc[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[c], sc[kb2], 0, 0, 0);
-                    }
-                }
-            };
-            floatx16 sc[NKB];
-            half8 pop[2 * NKB];
-#pragma unroll
-            for (int kb2 = 0; kb2 < NKB; ++kb2)
+            for (int kb2 = 0; kb2 < NKB; ++kb2) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) sc[kb2][i] = 0.f;
 #pragma unroll
-            for (int t = 0; t < 2 * NKB; ++t) pop[t] = half8{};
+                for (int c = 0; c < NC; ++c) {
+                    const half8 kop = *reinterpret_cast<const half8*>(&Kt[kro[c] + 32 * kb2 * D]);
+                    sc[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[c], sc[kb2], 0, 0, 0);
+                }
+            }
+        };
+        floatx16 sc[NKB];
+        half8 pop[2 * NKB];
+#pragma unroll
+        for (int kb2 = 0; kb2 < NKB; ++kb2)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[kb2][i] = 0.f;
+#pragma unroll
+        for (int t = 0; t < 2 * NKB; ++t) pop[t] = half8{};
 
-            // Ping-pong (long prompts): the two wave groups (waves 0-3, 4-7; one
-            // wave of each per SIMD) alternate an MFMA step and a softmax step,
-            // group 1 one phase behind group 0.  The barriers order memory only,
-            // so the compiler may still move a step's ALU work across them; the
-            // MFMA step's operand reads are scheduled PF ahead of their MFMAs.
-            // Measured at S=8192: 3-4 % faster than the loop below; at S=2048
-            // (KG == 2) 2 % slower, so short prompts keep that loop.
-            //   mstep(j): S^T(j) = K(j) Q^T (j < n),  O^T += V(j-1)^T P(j-1)^T (j >= 1)
-            //   sstep(j): P(j) from S^T(j); O, l rescaled when the max moves.
-            // Phase 2j: group 0 mstep(j), group 1 sstep(j-1); phase 2j+1: group 0
-            // sstep(j), group 1 mstep(j); one workgroup barrier between phases.
-            // Ring: tile j+2 is issued at the start of phase 2j into the stage
-            // of tile j-2, whose last reader (group 1's mstep(j-1)) ran in phase
-            // 2j-1; before the barrier into phase 2j each wave waits for its own
-            // DMA of tile j (tile j+1 may stay in flight).  Tiles past the end
-            // re-load the last tile, so every wave issues the same loads.
-            auto pv = [&](int j) {
-                const f16* Vt = ring + (j % NSTAGE) * 2 * TB + TB;
+        // Ping-pong: the two wave groups (waves 0-3, 4-7; one wave of each per
+        // SIMD; with KG = 2 the two key halves of every tile) alternate an
+        // MFMA step and a softmax step, group 1 one phase behind group 0, so
+        // that one wave's MFMAs run under the other's exponentials.  The
+        // barriers order memory only, so the compiler may still move a step's
+        // ALU work across them; the MFMA step's operand reads are scheduled PF
+        // ahead of their MFMAs.  With the MFMA step at wave priority 1 this
+        // beats a plain per-tile loop (QK of tile t+1, softmax of t, PV of t in
+        // every wave) at every size: S=2048 45.4 vs 47.1 us, S=8192 516 vs
+        // 540 us.
+        //   mstep(j): S^T(j) = K(j) Q^T (j < n),  O^T += V(j-1)^T P(j-1)^T (j >= 1)
+        //   sstep(j): P(j) from S^T(j); O, l rescaled when the max moves.
+        // Phase 2j: group 0 mstep(j), group 1 sstep(j-1); phase 2j+1: group 0
+        // sstep(j), group 1 mstep(j); one workgroup barrier between phases.
+        // Ring: tile j+2 is issued at the start of phase 2j into the stage
+        // of tile j-2, whose last reader (group 1's mstep(j-1)) ran in phase
+        // 2j-1; before the barrier into phase 2j each wave waits for its own
+        // DMA of tile j (tile j+1 may stay in flight).  Tiles past the end
+        // re-load the last tile, so every wave issues the same loads.
+        auto pv = [&](int j) {
+            const f16* Vt = ring + (j % NSTAGE) * 2 * TB + TB;
 #pragma unroll
-                for (int t = 0; t < 2 * NKB; ++t) {
+            for (int t = 0; t < 2 * NKB; ++t) {
 #pragma unroll
-                    for (int db = 0; db < NDB; ++db) {
-                        const f16* p1 = &Vt[vro[db] + 16 * t * D];
-                        const half8 vop = cat_half8(lds_read_tr16(p1), lds_read_tr16(p1 + 8 * D));
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pop[t], o[db], 0, 0, 0);
-                    }
+                for (int db = 0; db < NDB; ++db) {
+                    const f16* p1 = &Vt[vro[db] + 16 * t * D];
+                    const half8 vop = cat_half8(lds_read_tr16(p1), lds_read_tr16(p1 + 8 * D));
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pop[t], o[db], 0, 0, 0);
                 }
-            };
-            // Operand reads run PF reads ahead of the MFMAs that use them.
-            constexpr int NQK = NKB * NC, NPV = 2 * NKB * NDB;   // MFMAs
-            constexpr int PF = 8;
-            // The MFMA step runs at wave priority 1: when the SIMD's other wave
-            // (softmax step) and this one both can issue, the MFMAs go first
-            // (S=8192 516 vs 524 us; the key-split loop gains nothing from it).
-            auto mstep = [&](int j) {   // 1 <= j < n_tiles
-                __builtin_amdgcn_s_setprio(1);
-                qk(ring + (j % NSTAGE) * 2 * TB, sc);
-                pv(j - 1);
-                __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+            }
+        };
+        // Operand reads run PF reads ahead of the MFMAs that use them.
+        constexpr int NQK = NKB * NC, NPV = 2 * NKB * NDB;   // MFMAs
+        constexpr int PF = 8;
+        // The MFMA step runs at wave priority 1: when the SIMD's other wave
+        // (softmax step) and this one both can issue, the MFMAs go first
+        // (S=8192 516 vs 524 us, S=2048 45.4 vs 47.2 us).
+        auto mstep = [&](int j) {   // 1 <= j < n_tiles
+            __builtin_amdgcn_s_setprio(1);
+            qk(ring + (j % NSTAGE) * 2 * TB, sc);
+            pv(j - 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
 #pragma unroll
-                for (int i = 0; i < NQK - PF; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
+            for (int i = 0; i < NQK - PF; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
 #pragma unroll
-                for (int i = 0; i < NPV; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                }
-                __builtin_amdgcn_sched_group_barrier(0x008, NQK + NPV - (NQK - PF) - NPV, 0);
-                __builtin_amdgcn_s_setprio(0);
-            };
-            auto sstep = [&](int j) {
-                const int k0 = j * kBN;
-                const bool act = uvalid && k0 <= r0 + 31;
-                // ---- online softmax of query row `row`; P^T operands straight
-                // from S^T.  Inactive units (invalid, or entirely above the
-                // diagonal) see only -inf scores: alpha = 1 and p = 0 leave their
-                // state as is.  The running max is kept on raw scores and the
-                // scale folded into the exponent.
-                if (!act || k0 + kBN - 1 > r0) {
-                    // element (kb2, i) holds key k0 + 32(kb2 + kgrp) + 4h +
-                    // 8(i/4) + i%4; keys past min(row, S-1) are masked
-                    const int lim = act ? min(row, S - 1) - (k0 + 32 * kgrp + 4 * h) : -1;
-#pragma unroll
-                    for (int kb2 = 0; kb2 < NKB; ++kb2)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i)
-                            if (32 * kb2 + 8 * (i / 4) + (i % 4) > lim) sc[kb2][i] = -INFINITY;
-                }
-                float tmax = -INFINITY;
+            for (int i = 0; i < NPV; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NQK + NPV - (NQK - PF) - NPV, 0);
+            __builtin_amdgcn_s_setprio(0);
+        };
+        auto sstep = [&](int j) {
+            const int k0 = j * kBN;
+            const bool act = uvalid && k0 <= r0 + 31;
+            // ---- online softmax of query row `row`; P^T operands straight
+            // from S^T.  Inactive units (invalid, or entirely above the
+            // diagonal) see only -inf scores: alpha = 1 and p = 0 leave their
+            // state as is.  The running max is kept on raw scores and the
+            // scale folded into the exponent.
+            if (!act || k0 + kBN - 1 > r0) {
+                // element (kb2, i) holds key k0 + 32(kb2 + kgrp) + 4h +
+                // 8(i/4) + i%4; keys past min(row, S-1) are masked
+                const int lim = act ? min(row, S - 1) - (k0 + 32 * kgrp + 4 * h) : -1;
 #pragma unroll
                 for (int kb2 = 0; kb2 < NKB; ++kb2)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sc[kb2][i]);
-                tmax = halves_max(tmax);
-                // Lazy rescale: m_run is a reference max, moved (and O, l
-                // rescaled) only when some row's max exceeds it by more than
-                // kLazyLog2 in log2 units; otherwise p = 2^(s*c - m_run*c) stays
-                // below 2^kLazyLog2, exact in fp16.
-                if (__builtin_amdgcn_read_exec() & __ballot(tmax > m_run + lazy_thr)) {
-                    const float mn = fmaxf(m_run, tmax);
-                    const float alpha = fast_exp2((m_run - mn) * a.scale_log2);
-                    l_part *= alpha;
-#pragma unroll
-                    for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-                    m_run = mn;
-                }
-                const float nmc = -m_run * a.scale_log2;
-#pragma unroll
-                for (int t = 0; t < 2 * NKB; ++t)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        pop[t][e] = static_cast<f16>(
-                            fast_exp2(fmaf(sc[t / 2][8 * (t % 2) + e], a.scale_log2, nmc)));
-                // Row sum of the fp16 P actually fed to the PV contraction, two
-                // values per v_dot2_f32_f16 with fp32 accumulation.
-                const half2v ones = {static_cast<f16>(1.f), static_cast<f16>(1.f)};
-#pragma unroll
-                for (int t = 0; t < 2 * NKB; ++t)
-#pragma unroll
-                    for (int e = 0; e < 8; e += 2)
-                        l_part = __builtin_amdgcn_fdot2(half2v{pop[t][e], pop[t][e + 1]}, ones, l_part,
-                                                        false);
-            };
-            auto phase_start = [&](int j) {   // barrier into phase 2j, then tile j+2
-                wait_vmcnt<LPT>();
-                ring_barrier();
-                const int tt = j + 2;
-                issue(ring + (tt % NSTAGE) * 2 * TB, tt);
-            };
-            if ((wave >> 2) == 0) {
-                phase_start(0);
-                qk(ring, sc);
-                ring_barrier();
-                sstep(0);
-                for (int j = 1; j < n_tiles; ++j) {
-                    phase_start(j);
-                    mstep(j);
-                    ring_barrier();
-                    sstep(j);
-                }
-                phase_start(n_tiles);
-                pv(n_tiles - 1);
-                ring_barrier();
-            } else {
-                phase_start(0);
-                ring_barrier();
-                qk(ring, sc);
-                for (int j = 1; j < n_tiles; ++j) {
-                    phase_start(j);
-                    sstep(j - 1);
-                    ring_barrier();
-                    mstep(j);
-                }
-                phase_start(n_tiles);
-                sstep(n_tiles - 1);
-                ring_barrier();
-                pv(n_tiles - 1);
+                    for (int i = 0; i < 16; ++i)
+                        if (32 * kb2 + 8 * (i / 4) + (i % 4) > lim) sc[kb2][i] = -INFINITY;
             }
-        } else {
-            wait_vmcnt<0>();  // q in registers before the ring: no compiler waits inside it
-            ring_barrier();   // everyone is done with the previous pass's stages
-            issue(ring, 0);
-            issue(ring + 2 * TB, 1);
-            issue(ring + 4 * TB, 2);
-
-            // Software pipeline: step kt computes S^T of tile kt+1 (MFMA) before
-            // the softmax of tile kt (VALU), so the matrix cores work while the
-            // exponentials run, then O^T += V^T P^T for tile kt.  Step kt needs
-            // K of tile kt+1 and V of tile kt: wait for this wave's DMA of tile
-            // kt+1 (tile kt+2 stays in flight), barrier (all waves' DMA landed,
-            // the stage of tile kt-1 is free), refill that stage with tile kt+3.
-            constexpr int NKB = 2 / KG;     // this wave's 32-key blocks per tile
-            auto qk = [&](const f16* Kt, floatx16 (&sc)[NKB]) {
+            float tmax = -INFINITY;
 #pragma unroll
-                for (int kb2 = 0; kb2 < NKB; ++kb2) {
+            for (int kb2 = 0; kb2 < NKB; ++kb2)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) sc[kb2][i] = 0.f;
+                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sc[kb2][i]);
+            tmax = halves_max(tmax);
+            // Lazy rescale: m_run is a reference max, moved (and O, l
+            // rescaled) only when some row's max exceeds it by more than
+            // kLazyLog2 in log2 units; otherwise p = 2^(s*c - m_run*c) stays
+            // below 2^kLazyLog2, exact in fp16.
+            if (__builtin_amdgcn_read_exec() & __ballot(tmax > m_run + lazy_thr)) {
+                const float mn = fmaxf(m_run, tmax);
+                const float alpha = fast_exp2((m_run - mn) * a.scale_log2);
+                l_part *= alpha;
 #pragma unroll
-                    for (int c = 0; c < NC; ++c) {
-                        const half8 kop = *reinterpret_cast<const half8*>(&Kt[kro[c] + 32 * kb2 * D]);
-                        sc[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[c], sc[kb2], 0, 0, 0);
-                    }
-                }
-            };
-
-            floatx16 scur[NKB], snext[NKB];
-            wait_vmcnt<2 * LPT>();
+                for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+                m_run = mn;
+            }
+            const float nmc = -m_run * a.scale_log2;
+#pragma unroll
+            for (int t = 0; t < 2 * NKB; ++t)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    pop[t][e] = static_cast<f16>(
+                        fast_exp2(fmaf(sc[t / 2][8 * (t % 2) + e], a.scale_log2, nmc)));
+            // Row sum of the fp16 P actually fed to the PV contraction, two
+            // values per v_dot2_f32_f16 with fp32 accumulation.
+            const half2v ones = {static_cast<f16>(1.f), static_cast<f16>(1.f)};
+#pragma unroll
+            for (int t = 0; t < 2 * NKB; ++t)
+#pragma unroll
+                for (int e = 0; e < 8; e += 2)
+                    l_part = __builtin_amdgcn_fdot2(half2v{pop[t][e], pop[t][e + 1]}, ones, l_part,
+                                                    false);
+        };
+        auto phase_start = [&](int j) {   // barrier into phase 2j, then tile j+2
+            wait_vmcnt<LPT>();
             ring_barrier();
-            qk(ring, scur);
-
-            for (int kt = 0; kt < n_tiles; ++kt) {
-                const f16* cur = ring + (kt % NSTAGE) * 2 * TB;
-                wait_vmcnt<LPT>();
+            const int tt = j + 2;
+            issue(ring + (tt % NSTAGE) * 2 * TB, tt);
+        };
+        if ((wave >> 2) == 0) {
+            phase_start(0);
+            qk(ring, sc);
+            ring_barrier();
+            sstep(0);
+            for (int j = 1; j < n_tiles; ++j) {
+                phase_start(j);
+                mstep(j);
                 ring_barrier();
-                issue(ring + ((kt + NSTAGE - 1) % NSTAGE) * 2 * TB, kt + 3);
-                // tile kt+1 (the last tile again past the end: its result unused)
-                qk(ring + ((kt + 1) % NSTAGE) * 2 * TB, snext);
-
-                const int k0 = kt * kBN;
-                const bool act = uvalid && k0 <= r0 + 31;
-                // ---- online softmax of query row `row`; P^T operands straight
-                // from S^T.  Inactive units (invalid, or entirely above the
-                // diagonal) see only -inf scores: alpha = 1 and p = 0 leave their
-                // state as is, so every MFMA runs unconditionally (no branches,
-                // no conservative waits inside the ring).  The running max is
-                // kept on raw scores and the scale folded into the exponent.
-                if (!act || k0 + kBN - 1 > r0) {
-#pragma unroll
-                    for (int kb2 = 0; kb2 < NKB; ++kb2)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            const int key = k0 + 32 * (kb2 + kgrp) + 8 * (i / 4) + 4 * h + (i % 4);
-                            if (!act || key > row || key >= S) scur[kb2][i] = -INFINITY;
-                        }
-                }
-                float tmax = -INFINITY;
-#pragma unroll
-                for (int kb2 = 0; kb2 < NKB; ++kb2)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, scur[kb2][i]);
-                tmax = halves_max(tmax);
-                // Lazy rescale: m_run is a reference max, moved (and O, l
-                // rescaled) only when some row's max exceeds it by more than
-                // kLazyLog2 in log2 units; otherwise p = 2^(s*c - m_run*c) stays
-                // below 2^kLazyLog2, exact in fp16.  A wave-uniform branch taken
-                // on the first tiles and rarely after.
-                if (__builtin_amdgcn_read_exec() & __ballot(tmax > m_run + lazy_thr)) {
-                    const float mn = fmaxf(m_run, tmax);
-                    const float alpha = fast_exp2((m_run - mn) * a.scale_log2);
-                    l_part *= alpha;
-#pragma unroll
-                    for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-                    m_run = mn;
-                }
-                const float nmc = -m_run * a.scale_log2;
-                half8 pop[2 * NKB];
-#pragma unroll
-                for (int t = 0; t < 2 * NKB; ++t)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        pop[t][e] = static_cast<f16>(
-                            fast_exp2(fmaf(scur[t / 2][8 * (t % 2) + e], a.scale_log2, nmc)));
-                // Row sum of the fp16 P actually fed to the PV contraction, two
-                // values per v_dot2_f32_f16 with fp32 accumulation.
-                const half2v ones = {static_cast<f16>(1.f), static_cast<f16>(1.f)};
-#pragma unroll
-                for (int t = 0; t < 2 * NKB; ++t)
-#pragma unroll
-                    for (int e = 0; e < 8; e += 2)
-                        l_part = __builtin_amdgcn_fdot2(half2v{pop[t][e], pop[t][e + 1]}, ones, l_part,
-                                                        false);
-
-                // ---- O^T += V^T P^T: lane j16 of 16-lane block (h, blk2) reads
-                //      rows R(j16/4) at dims 32db + 16*blk2 + 4*(j16%4).
-                const f16* Vt = cur + TB;
-#pragma unroll
-                for (int t = 0; t < 2 * NKB; ++t) {
-#pragma unroll
-                    for (int db = 0; db < NDB; ++db) {
-                        const f16* p1 = &Vt[vro[db] + 16 * t * D];
-                        const half8 vop = cat_half8(lds_read_tr16(p1), lds_read_tr16(p1 + 8 * D));
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pop[t], o[db], 0, 0, 0);
-                    }
-                }
-#pragma unroll
-                for (int kb2 = 0; kb2 < NKB; ++kb2) scur[kb2] = snext[kb2];
+                sstep(j);
             }
+            phase_start(n_tiles);
+            pv(n_tiles - 1);
+            ring_barrier();
+        } else {
+            phase_start(0);
+            ring_barrier();
+            qk(ring, sc);
+            for (int j = 1; j < n_tiles; ++j) {
+                phase_start(j);
+                sstep(j - 1);
+                ring_barrier();
+                mstep(j);
+            }
+            phase_start(n_tiles);
+            sstep(n_tiles - 1);
+            ring_barrier();
+            pv(n_tiles - 1);
         }
         wait_vmcnt<0>();  // drain the ring's trailing re-loads
 
