@@ -372,8 +372,9 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
 // as the A operand.  A tile is 16 weight rows; for the paired epilogues its
 // first 8 rows pair with its last 8 (SwiGLU: gate rows n..n+7 with up rows
 // N+n..N+n+7; RoPE: dims d..d+7 with d+D/2..d+D/2+7 of one head).  The NW
-// waves of a workgroup split K into slices of 32*C (wave w: k in
-// [32Cw, 32C(w+1))) and keep their slice of X (all B rows: NBT tiles of 16,
+// waves of a workgroup split K into slices of 32*C (slice s: k in
+// [32Cs, 32C(s+1)), wave w taking slice (w + rot) % NW with rot chosen per
+// workgroup) and keep their slice of X (all B rows: NBT tiles of 16,
 // zero past B; RMSNorm applied once) in registers, while the workgroup walks
 // tiles blockIdx.x, +gridDim.x, ... (grid = the resident workgroups): the
 // next tile's weights are loaded before the current tile's MFMAs, and the
@@ -382,7 +383,7 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
 // l%16) loads row col of a tile at k = 32t + 8g (16 bytes; an instruction
 // reads 64 contiguous bytes of 16 rows) and the same k of batch row col; the
 // accumulator holds D[4g + e][col].  The NW partial tiles meet in LDS (two
-// buffers, one barrier per tile) and are summed in wave order
+// buffers, one barrier per tile) and are summed in slice order
 // (deterministic), then the batch-1 GEMV's epilogue runs per (row, batch
 // row).  RMSNorm: the waves' sums of squares of their slices meet in LDS
 // first, so the operand is fp16(x * rs * w) as the batch-1 kernel rounds it.
