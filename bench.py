@@ -527,6 +527,11 @@ def run_kv_movement(torch, kvhp):
 
 
 def run_config1(torch, kvhp):
+    """BASELINE config 1 as the reference's two calls (append_kv_cache, then
+    decode_gqa), and as one kvhp_append_decode call on the same cache viewed
+    strided (the covering split writes the row, then attends it); both timed
+    warm (100 eager steps back to back), replayed from a HIP graph and as
+    flushed single steps.  The fused step's output equals the two calls'."""
     hq, hkv, d, max_seq = 32, 8, 64, 512
     g = torch.Generator(device="cuda").manual_seed(1)
     kc = torch.randn((hkv, max_seq, d), generator=g, device="cuda").half()
@@ -535,75 +540,93 @@ def run_config1(torch, kvhp):
     vn = torch.randn((1, hkv, d), generator=g, device="cuda").half()
     q = torch.randn((1, hq, d), generator=g, device="cuda").half()
     out = torch.empty((1, hq, d), dtype=torch.float16, device="cuda")
+    out_f = torch.empty_like(out)
+    kview = kvhp.strided_view(kc, hkv * max_seq * d, max_seq * d, d)
+    vview = kvhp.strided_view(vc, hkv * max_seq * d, max_seq * d, d)
+    pos = torch.tensor([511], dtype=torch.int32, device="cuda")
+    lens = torch.tensor([512], dtype=torch.int32, device="cuda")
 
     def step():
         kvhp.append_kv(kn, vn, kc, vc, 1, 511, hkv, max_seq, d)
         kvhp.decode_gqa(q, kc, vc, out, 512, hq, hkv, max_seq, d)
 
-    for _ in range(10):
-        step()
-    # warm: 100 steps back to back under one event pair (an event pair and a
-    # host wait per step would leave the GPU idle between 15-us steps, so its
-    # clocks would drop and "warm" would read slower than flushed)
+    def fused():
+        kvhp.append_decode(q, kn, vn, kview, vview, pos, lens, out_f, hq, hkv, d, max_seq)
+
     stream = torch.cuda.current_stream()
-    warm = []
-    for _ in range(5):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(100):
-            step()
-        e1.record(stream)
-        e1.synchronize()
-        warm.append(e0.elapsed_time(e1) * 1e3 / 100)
-    warm_t = (float(np.median(warm)), float(np.mean(warm)), float(np.min(warm)), float(np.max(warm)))
-    # The same 100 steps replayed from one HIP graph: launched eagerly, a
-    # ~12 us step is bounded by the host's launch rate, not the GPU.  The
-    # graph's output must equal an eager step's bit for bit.
-    graph_t = None
-    try:
-        g = torch.cuda.CUDAGraph()
-        cap = torch.cuda.Stream()
-        cap.wait_stream(stream)
-        with torch.cuda.graph(g, stream=cap, capture_error_mode="thread_local"):
-            for _ in range(100):
-                step()
-        stream.wait_stream(cap)
-        torch.cuda.synchronize()
-        out.zero_()
-        g.replay()
-        torch.cuda.synchronize()
-        from_graph = out.clone()
-        out.zero_()
-        step()
-        torch.cuda.synchronize()
-        if torch.equal(from_graph, out):
-            gt = []
-            for _ in range(5):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                g.replay()
-                e1.record(stream)
-                e1.synchronize()
-                gt.append(e0.elapsed_time(e1) * 1e3 / 100)
-            graph_t = (float(np.median(gt)), float(np.mean(gt)), float(np.min(gt)), float(np.max(gt)))
-        else:
-            log("config1 graph output differs from an eager step: not reported")
-        del g
-    except Exception as exc:  # capture unsupported here: eager figures only
-        log(f"config1 graph capture failed: {exc}")
     fl = Flusher(torch)
-    cold = time_op(torch, step, 20, fl)
+
+    def timings(fn, dst):
+        for _ in range(10):
+            fn()
+        # warm: 100 steps back to back under one event pair (an event pair and a
+        # host wait per step would leave the GPU idle between 15-us steps, so its
+        # clocks would drop and "warm" would read slower than flushed)
+        warm = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(100):
+                fn()
+            e1.record(stream)
+            e1.synchronize()
+            warm.append(e0.elapsed_time(e1) * 1e3 / 100)
+        warm_t = (float(np.median(warm)), float(np.mean(warm)), float(np.min(warm)),
+                  float(np.max(warm)))
+        # The same 100 steps replayed from one HIP graph: launched eagerly, a
+        # ~12 us step is bounded by the host's launch rate, not the GPU.  The
+        # graph's output must equal an eager step's bit for bit.
+        graph_t = None
+        try:
+            gr = torch.cuda.CUDAGraph()
+            cap = torch.cuda.Stream()
+            cap.wait_stream(stream)
+            with torch.cuda.graph(gr, stream=cap, capture_error_mode="thread_local"):
+                for _ in range(100):
+                    fn()
+            stream.wait_stream(cap)
+            torch.cuda.synchronize()
+            dst.zero_()
+            gr.replay()
+            torch.cuda.synchronize()
+            from_graph = dst.clone()
+            dst.zero_()
+            fn()
+            torch.cuda.synchronize()
+            if torch.equal(from_graph, dst):
+                gt = []
+                for _ in range(5):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    gr.replay()
+                    e1.record(stream)
+                    e1.synchronize()
+                    gt.append(e0.elapsed_time(e1) * 1e3 / 100)
+                graph_t = (float(np.median(gt)), float(np.mean(gt)), float(np.min(gt)),
+                           float(np.max(gt)))
+            else:
+                log("config1 graph output differs from an eager step: not reported")
+            del gr
+        except Exception as exc:  # capture unsupported here: eager figures only
+            log(f"config1 graph capture failed: {exc}")
+        cold = time_op(torch, fn, 20, fl)
+        r = {"us_per_step_flushed": round(cold[0], 2), "flushed": spread(cold),
+             "us_per_step_warm": round(warm_t[0], 2),
+             "warm": {**spread(warm_t), "note": "median of 5 runs of 100 back-to-back steps, "
+                                                "eager launches"}}
+        if graph_t is not None:
+            r["us_per_step_graph"] = round(graph_t[0], 2)
+            r["graph"] = {**spread(graph_t), "note": "median of 5 replays of one HIP graph of "
+                                                     "100 steps"}
+        return r
+
     res = {"workload": "config1: append 1 token at pos 511 + decode ctx 512, 32/8 heads, D=64 "
                        "(the reference's two calls: append_kv_cache, decode_gqa)",
-           "us_per_step_flushed": round(cold[0], 2), "flushed": spread(cold),
-           "us_per_step_warm": round(warm_t[0], 2),
-           "warm": {**spread(warm_t), "note": "median of 5 runs of 100 back-to-back steps, "
-                                              "eager launches"},
-           "bytes": decode_bytes([512], hq, hkv, d) + append_bytes(1, hkv, d)}
-    if graph_t is not None:
-        res["us_per_step_graph"] = round(graph_t[0], 2)
-        res["graph"] = {**spread(graph_t), "note": "median of 5 replays of one HIP graph of "
-                                                   "100 steps"}
+           **timings(step, out), "bytes": decode_bytes([512], hq, hkv, d) + append_bytes(1, hkv, d)}
+    res["fused"] = {"workload": "the same step as one kvhp_append_decode call on strided views",
+                    **timings(fused, out_f)}
+    torch.cuda.synchronize()
+    res["fused"]["output_equals_two_calls"] = bool(torch.equal(out, out_f))
     return res
 
 

@@ -198,6 +198,17 @@ int kvhp_paged_append_decode(const void* q, const void* k_new, const void* v_new
                              int batch, int num_q_heads, int num_kv_heads, int head_dim,
                              int max_seq_len, int num_splits, void* workspace,
                              size_t workspace_bytes, void* stream);
+/* The same pair on views of either kind: paged views as
+ * kvhp_paged_append_decode; strided views (the reference KVCache layout,
+ * src/runtime/kv_cache.cu:8-36 then decode_attention_split.cu:183-214) get
+ * row positions[b] of sequence b written, positions outside
+ * [0, max_seq_len) dropped as the reference append drops those past
+ * max_seq.  One launch (plus the merge) within the fast kernel's shapes. */
+int kvhp_append_decode(const void* q, const void* k_new, const void* v_new,
+                       const kvhp_kv_view* k_view, const kvhp_kv_view* v_view,
+                       const int32_t* positions, const int32_t* seq_lens, void* out, int batch,
+                       int num_q_heads, int num_kv_heads, int head_dim, int max_seq_len,
+                       int num_splits, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Replaces engine::cuda::decode_gqa (src/cuda/kernels.h:104-115,
  * src/cuda/decode_attention.cu:114-137): one sequence, head-major cache

@@ -91,9 +91,10 @@ struct DecodeArgs {
     int cap;               // tokens addressable per sequence
     int fixed_len;         // length of every sequence when seq_lens == nullptr
     float scale_log2;      // log2(e) / sqrt(D)
-    // Fused append (paged only; k_new == nullptr: none): row b of k_new /
-    // v_new [B][Hkv][D] is the token at position new_pos[b]; the split that
-    // covers it writes it into its page before reading the page.
+    // Fused append (k_new == nullptr: none): row b of k_new / v_new
+    // [B][Hkv][D] is the token at position new_pos[b]; the split that covers
+    // it writes it into its page (or its row of a strided view) before
+    // reading it.
     const f16* k_new;
     const f16* v_new;
     const int32_t* new_pos;
@@ -248,18 +249,18 @@ decode_splitk_kernel(const DecodeArgs a) {
     const int nsb = L > 0 ? (L + chunk - 1) / chunk : 0;
 
     // Fused append: the split that covers the new position (the last split
-    // if it lies beyond them) writes the row into its page before its first
-    // K/V load and waits for the stores to complete, so its own loads of that
-    // row return it -- the reference appends before it attends
-    // (forward_gpu.cu:593-640), and only this workgroup reads that row.
-    // Invalid positions and page ids are dropped as by kvhp_paged_append_kv.
+    // if it lies beyond them) writes the row into its page (strided views:
+    // its row) before its first K/V load and waits for the stores to
+    // complete, so its own loads of that row return it -- the reference
+    // appends before it attends (forward_gpu.cu:593-640), and only this
+    // workgroup reads that row.  Invalid positions and page ids are dropped
+    // as by kvhp_paged_append_kv; on a strided view positions at or past the
+    // call's capacity, as kvhp_append_kv drops those past max_seq.
     int app_pos = -1;
-    if constexpr (PAGED) {
-        if (a.k_new) {
-            const int p = a.new_pos[b];
-            const int last = a.balance > 0 ? max(nsb, 1) - 1 : a.nsplit - 1;
-            if (p >= 0 && split == min(p / chunk, last)) app_pos = p;
-        }
+    if (a.k_new) {
+        const int p = a.new_pos[b];
+        const int last = a.balance > 0 ? max(nsb, 1) - 1 : a.nsplit - 1;
+        if (p >= 0 && split == min(p / chunk, last)) app_pos = p;
     }
     // Splits past the sequence's keys stop here (before any page-table
     // load), except the one that appends.
@@ -291,6 +292,19 @@ decode_splitk_kernel(const DecodeArgs a) {
                                     ((int64_t)pid * kPage + (p & 15)) * a.k.stride_s + 8 * lane;
                 store_half8(a.pool_k + dst, load_half8(a.k_new + src));
                 store_half8(a.pool_v + dst, load_half8(a.v_new + src));
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+    } else {
+        if (app_pos >= 0) {
+            const int p = app_pos;
+            constexpr int LPR0 = D / 8;
+            if (p < a.cap && lane < LPR0) {
+                const int64_t src = ((int64_t)b * a.Hkv + kvh) * D + 8 * lane;
+                const int64_t dk = b * a.k.stride_b + kvh * a.k.stride_h + p * a.k.stride_s + 8 * lane;
+                const int64_t dv = b * a.v.stride_b + kvh * a.v.stride_h + p * a.v.stride_s + 8 * lane;
+                store_half8(a.pool_k + dk, load_half8(a.k_new + src));
+                store_half8(a.pool_v + dv, load_half8(a.v_new + src));
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
@@ -777,6 +791,25 @@ decode_merge_rows_kernel(const DecodeArgs a) {
     store_half8(a.out + row * D + 8 * c, hv);
 }
 
+// Append of one token per sequence into strided views (the fused append's
+// fallback outside the fast kernel's shapes): element (b, h, d) of k_new /
+// v_new [B][Hkv][D] to row new_pos[b] of sequence b, head h; positions
+// outside [0, cap) are dropped.
+__global__ void __launch_bounds__(256)
+append_rows_strided_kernel(const f16* k_new, const f16* v_new, const KVDev k, const KVDev v,
+                           const int32_t* new_pos, int batch, int hkv, int D, int cap,
+                           f16* dst_k, f16* dst_v) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)batch * hkv * D) return;
+    const int d = static_cast<int>(i % D);
+    const int h = static_cast<int>((i / D) % hkv);
+    const int b = static_cast<int>(i / ((int64_t)D * hkv));
+    const int p = new_pos[b];
+    if (p < 0 || p >= cap) return;
+    dst_k[b * k.stride_b + h * k.stride_h + p * k.stride_s + d * k.stride_d] = k_new[i];
+    dst_v[b * v.stride_b + h * v.stride_h + p * v.stride_s + d * v.stride_d] = v_new[i];
+}
+
 // Any head_dim <= 256, any group size, any page size, any strides: one wave
 // per (q_head, sequence), one pass over the keys with an online softmax.
 // Serves shapes outside the fast kernel's template set.
@@ -1125,18 +1158,28 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
                       view_fast_ok(*vv) && aligned16(q) && aligned16(out) && shared_table &&
                       plan.nsplit <= kMaxSplits;
     if (k_new) {
-        KVHP_REQUIRE(paged && v_new && new_pos, KVHP_ERR_INVALID,
-                     "append_decode: paged views, k_new, v_new and positions required");
+        KVHP_REQUIRE(v_new && new_pos, KVHP_ERR_INVALID,
+                     "append_decode: k_new, v_new and positions required");
         if (fast && aligned16(k_new) && aligned16(v_new)) {
             a.k_new = static_cast<const f16*>(k_new);
             a.v_new = static_cast<const f16*>(v_new);
             a.new_pos = new_pos;
-        } else {
+        } else if (paged) {
             // outside the fused kernel's shapes: the append, then attention
             rc = kvhp_paged_append_kv(k_new, v_new, const_cast<void*>(kv->data),
                                       const_cast<void*>(vv->data), kv->block_table,
                                       kv->max_pages, new_pos, batch, 1, hkv, d, kv->num_pages,
                                       s);
+            if (rc) return rc;
+        } else {
+            const int64_t n = (int64_t)batch * hkv * d;
+            hipLaunchKernelGGL(append_rows_strided_kernel, dim3((unsigned)((n + 255) / 256)),
+                               dim3(256), 0, s, static_cast<const f16*>(k_new),
+                               static_cast<const f16*>(v_new), to_dev(*kv), to_dev(*vv), new_pos,
+                               batch, hkv, d, max_seq_len,
+                               const_cast<f16*>(static_cast<const f16*>(kv->data)),
+                               const_cast<f16*>(static_cast<const f16*>(vv->data)));
+            rc = check_launch("append_decode");
             if (rc) return rc;
         }
     }
@@ -1288,6 +1331,21 @@ extern "C" int kvhp_paged_append_decode(const void* q, const void* k_new, const 
                  "append_decode: null pointer");
     KVHP_REQUIRE(k_view->block_table && v_view->block_table, KVHP_ERR_INVALID,
                  "append_decode: paged views required");
+    return decode_attention_impl(q, k_view, v_view, seq_lens, 0, out, batch, num_q_heads,
+                                 num_kv_heads, head_dim, max_seq_len, num_splits, workspace,
+                                 workspace_bytes, static_cast<hipStream_t>(stream), k_new, v_new,
+                                 positions);
+}
+
+extern "C" int kvhp_append_decode(const void* q, const void* k_new, const void* v_new,
+                                  const kvhp_kv_view* k_view, const kvhp_kv_view* v_view,
+                                  const int32_t* positions, const int32_t* seq_lens, void* out,
+                                  int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                  int max_seq_len, int num_splits, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+    clear_error();
+    KVHP_REQUIRE(seq_lens && k_new && v_new && positions && k_view && v_view, KVHP_ERR_INVALID,
+                 "append_decode: null pointer");
     return decode_attention_impl(q, k_view, v_view, seq_lens, 0, out, batch, num_q_heads,
                                  num_kv_heads, head_dim, max_seq_len, num_splits, workspace,
                                  workspace_bytes, static_cast<hipStream_t>(stream), k_new, v_new,

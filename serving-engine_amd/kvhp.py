@@ -80,6 +80,9 @@ _SIGNATURES = {
     "kvhp_paged_append_decode": (_i32, [_vp, _vp, _vp, ctypes.POINTER(KVView),
                                         ctypes.POINTER(KVView), _vp, _vp, _vp, _i32, _i32, _i32,
                                         _i32, _i32, _i32, _vp, _sz, _vp]),
+    "kvhp_append_decode": (_i32, [_vp, _vp, _vp, ctypes.POINTER(KVView), ctypes.POINTER(KVView),
+                                  _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz,
+                                  _vp]),
     "kvhp_decode_gqa": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "kvhp_flash_prefill": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "kvhp_flash_prefill_paged": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp,
@@ -308,6 +311,19 @@ def paged_append_decode(q, k_new, v_new, k_view: KVView, v_view: KVView, positio
     attention over seq_lens[b] keys (one call; paged views)."""
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _check(load().kvhp_paged_append_decode(
+        _ptr(q), _ptr(k_new), _ptr(v_new), ctypes.byref(k_view), ctypes.byref(v_view),
+        _ptr(positions), _ptr(seq_lens), _ptr(out), seq_lens.shape[0], num_q_heads,
+        num_kv_heads, head_dim, max_seq_len, num_splits, _ptr(workspace), ws_bytes,
+        _stream(stream)))
+
+
+def append_decode(q, k_new, v_new, k_view: KVView, v_view: KVView, positions, seq_lens, out,
+                  num_q_heads, num_kv_heads, head_dim, max_seq_len, num_splits=0, workspace=None,
+                  stream=None):
+    """paged_append_decode for views of either kind (strided views: row
+    positions[b] of sequence b, dropped outside [0, max_seq_len))."""
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(load().kvhp_append_decode(
         _ptr(q), _ptr(k_new), _ptr(v_new), ctypes.byref(k_view), ctypes.byref(v_view),
         _ptr(positions), _ptr(seq_lens), _ptr(out), seq_lens.shape[0], num_q_heads,
         num_kv_heads, head_dim, max_seq_len, num_splits, _ptr(workspace), ws_bytes,

@@ -450,6 +450,66 @@ def test_paged_append_decode_matches_separate_calls(hq, hkv, d, tiles):
     assert not torch.equal(pk2, pool_k), "nothing was appended"
 
 
+@pytest.mark.parametrize("hq,hkv,d,tiles", [(32, 8, 64, 1), (32, 8, 128, 1), (12, 4, 96, 1),
+                                            (32, 8, 128, 3), (32, 4, 64, 2)])
+def test_strided_append_decode_matches_separate_calls(hq, hkv, d, tiles):
+    """kvhp_append_decode on strided views (the reference KVCache layout,
+    [B][Hkv][cap][D]): the covering split writes row positions[b] and attends
+    it; against the row written separately followed by kvhp_decode_attention,
+    bit for bit on both caches and the outputs.  Ragged batch: an empty
+    sequence, a new position past the attended length (written, not
+    attended), one at the last row of the capacity, and one past it
+    (dropped, as the reference append drops positions past max_seq).  D=96
+    runs the fallback (append kernel, then the generic decode); the pattern
+    tiled 3 times (18 sequences) runs the balanced split list."""
+    import torch
+    rng = np.random.default_rng(600 + d + tiles)
+    cap = 2100
+    lens = np.tile(np.array([1000, 0, 511, 300, 2099, 2050], np.int32), tiles)  # cached tokens
+    b = lens.size
+    pos = lens.copy()
+    seq = lens + 1
+    seq[1::6] = 0                  # empty: row 0 written, output zeros
+    pos[3::6] = lens[3::6] + 4     # written, beyond the attended keys
+    seq[3::6] = lens[3::6]
+    pos[5::6] = cap + 7            # past the capacity: dropped
+    seq[5::6] = lens[5::6]
+    kc = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, cap, d)))
+    vc = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, cap, d)))
+    k_new = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, d)))
+    v_new = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, d)))
+    q = to_gpu_f16(oracle.normal_f16(rng, (b, hq, d)))
+    pos_t, seq_t = to_gpu(pos), to_gpu(seq)
+    note(f"strided append_decode Hq={hq} Hkv={hkv} D={d} lens={lens.tolist()}")
+
+    def views(k, v):
+        return (kvhp.strided_view(k, hkv * cap * d, cap * d, d),
+                kvhp.strided_view(v, hkv * cap * d, cap * d, d))
+
+    k1, v1 = kc.clone(), vc.clone()
+    for i in range(b):
+        if 0 <= pos[i] < cap:
+            k1[i, :, pos[i]] = k_new[i]
+            v1[i, :, pos[i]] = v_new[i]
+    out1 = torch.full((b, hq, d), float("nan"), dtype=torch.float16, device="cuda")
+    kv1, vv1 = views(k1, v1)
+    kvhp.decode_attention(q, kv1, vv1, seq_t, out1, hq, hkv, d, cap)
+    k2, v2 = kc.clone(), vc.clone()
+    out2 = torch.full((b, hq, d), float("nan"), dtype=torch.float16, device="cuda")
+    kv2, vv2 = views(k2, v2)
+    kvhp.append_decode(q, k_new, v_new, kv2, vv2, pos_t, seq_t, out2, hq, hkv, d, cap)
+    sync()
+    assert torch.equal(k1, k2) and torch.equal(v1, v2), "caches differ"
+    assert torch.equal(out1, out2), "outputs differ"
+    assert not torch.equal(k2, kc), "nothing was appended"
+    if tiles == 1:   # and against the oracle
+        ref = oracle.decode_attention(q.cpu().numpy().astype(np.float32),
+                                      k2.cpu().numpy().astype(np.float32),
+                                      v2.cpu().numpy().astype(np.float32), seq, hq, hkv, d,
+                                      nthreads=8)
+        assert_attn_close(out2.cpu().numpy(), ref, "strided append_decode")
+
+
 @pytest.mark.parametrize("stride_s", [(1 << 23) + 64, (1 << 24) + 8])
 def test_decode_row_pitch_beyond_24_bits(stride_s):
     """A strided view whose row pitch needs more than 24 bits (stride_s
