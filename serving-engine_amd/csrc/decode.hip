@@ -1108,7 +1108,7 @@ int validate_view(const kvhp_kv_view* v, const char* name) {
 }  // namespace
 
 // seq_lens == nullptr: every sequence has length fixed_len (host value).
-// k_new != nullptr: fused paged append (paged views only) -- row b of
+// k_new != nullptr: fused append (paged or strided views) -- row b of
 // k_new / v_new [B][Hkv][D] goes to position new_pos[b] before attention.
 int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_view* vv,
                           const int32_t* seq_lens, int fixed_len, void* out, int batch,
