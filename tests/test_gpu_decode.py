@@ -458,22 +458,25 @@ def test_strided_append_decode_matches_separate_calls(hq, hkv, d, tiles):
     it; against the row written separately followed by kvhp_decode_attention,
     bit for bit on both caches and the outputs.  Ragged batch: an empty
     sequence, a new position past the attended length (written, not
-    attended), one at the last row of the capacity, and one past it
-    (dropped, as the reference append drops positions past max_seq).  D=96
-    runs the fallback (append kernel, then the generic decode); the pattern
-    tiled 3 times (18 sequences) runs the balanced split list."""
+    attended), one at the last row of the capacity, one past it (dropped, as
+    the reference append drops positions past max_seq), and an idle row
+    (position -1: nothing written, its cached keys attended).  D=96 runs the
+    fallback (append kernel, then the generic decode); the pattern tiled 3
+    times (21 sequences) runs the balanced split list."""
     import torch
     rng = np.random.default_rng(600 + d + tiles)
     cap = 2100
-    lens = np.tile(np.array([1000, 0, 511, 300, 2099, 2050], np.int32), tiles)  # cached tokens
+    lens = np.tile(np.array([1000, 0, 511, 300, 2099, 2050, 700], np.int32), tiles)  # cached
     b = lens.size
     pos = lens.copy()
     seq = lens + 1
-    seq[1::6] = 0                  # empty: row 0 written, output zeros
-    pos[3::6] = lens[3::6] + 4     # written, beyond the attended keys
-    seq[3::6] = lens[3::6]
-    pos[5::6] = cap + 7            # past the capacity: dropped
-    seq[5::6] = lens[5::6]
+    seq[1::7] = 0                  # empty: row 0 written, output zeros
+    pos[3::7] = lens[3::7] + 4     # written, beyond the attended keys
+    seq[3::7] = lens[3::7]
+    pos[5::7] = cap + 7            # past the capacity: dropped
+    seq[5::7] = lens[5::7]
+    pos[6::7] = -1                 # idle: nothing written
+    seq[6::7] = lens[6::7]
     kc = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, cap, d)))
     vc = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, cap, d)))
     k_new = to_gpu_f16(oracle.normal_f16(rng, (b, hkv, d)))
