@@ -408,21 +408,24 @@ def test_paged_append_decode_matches_separate_calls(hq, hkv, d, tiles):
     kvhp_paged_append_kv followed by kvhp_decode_attention, bit for bit on
     both the pools and the outputs.  Ragged batch: an empty sequence, rows
     on page boundaries, a new position past the attended length (written,
-    not attended), and a new position on an unallocated page (dropped; no
+    not attended), a new position on an unallocated page (dropped; no
     attended key lies on an unallocated page, whose reads would alias
-    physical page 0 while other sequences write their rows).
+    physical page 0 while other sequences write their rows), and an idle
+    row (position -1: nothing written, its cached keys attended).
     D=96 runs the fallback (append kernel, then the generic decode).  The
-    pattern tiled 10 times (70 sequences) runs the balanced split list."""
+    pattern tiled 10 times (80 sequences) runs the balanced split list."""
     import torch
     rng = np.random.default_rng(500 + d + tiles)
-    lens = np.tile(np.array([1000, 0, 1, 15, 16, 300, 2047], np.int32), tiles)  # cached tokens
+    lens = np.tile(np.array([1000, 0, 1, 15, 16, 300, 2047, 700], np.int32), tiles)  # cached
     b = lens.size
     bt, P = make_block_tables(rng, lens + 8)
     pos = lens.copy()
     seq = lens + 1
-    pos[5::7] = lens[5::7] + 4    # written, beyond the attended keys
-    seq[5::7] = lens[5::7]
-    for i in range(4, b, 7):      # row 16 starts a page that has no id: the write is
+    pos[5::8] = lens[5::8] + 4    # written, beyond the attended keys
+    seq[5::8] = lens[5::8]
+    pos[7::8] = -1                # idle: nothing written
+    seq[7::8] = lens[7::8]
+    for i in range(4, b, 8):      # row 16 starts a page that has no id: the write is
         bt[i, pos[i] // 16] = -1  # dropped, and the 16 attended keys stay on page 0
         seq[i] = lens[i]
     pool_k = to_gpu_f16(oracle.normal_f16(rng, (hkv, P, 16, d)))
