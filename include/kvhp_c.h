@@ -173,7 +173,11 @@ int kvhp_decode_attention(const void* q, const kvhp_kv_view* k_view,
  * KVHP_ERR_WORKSPACE (config 3's auto plan needs 11.2 MB).  Every call on a
  * GPU shares that GPU's array: calls that overlap on one GPU (other streams
  * or threads) race.  Partials need no clearing: a call reads only the ones
- * it wrote. */
+ * it wrote.  The first call on a device resolves the array's address and
+ * its kernels' occupancy (no allocation, no stream work): make that first
+ * call, with the shapes to be captured, outside graph capture; later calls
+ * may be captured (tested: two calls in one graph, replays bit-identical to
+ * eager kvhp_decode_attention). */
 int kvhp_decode_attention_noalloc(const void* q, const kvhp_kv_view* k_view,
                                   const kvhp_kv_view* v_view, const int32_t* seq_lens,
                                   void* out, int batch, int num_q_heads, int num_kv_heads,
@@ -454,6 +458,18 @@ int kvhp_llama_decode_paged(void* model, const int32_t* tokens, int batch, void*
                             int num_pages, const int32_t* block_tables, int max_pages,
                             const int32_t* positions, const int32_t* seq_lens, int max_seq_len,
                             float* logits, int32_t* next_tokens, void* stream);
+/* Sizes the model's own decode buffers (split-attention partials, the
+ * batched down projection's K-split partials) for every kvhp_llama_decode_paged
+ * call with batch <= max_batch and max_seq_len <= max_seq_len, so that such
+ * calls allocate nothing.  No reference counterpart (the reference sizes its
+ * split buffer once at load, forward_gpu.cu:100).  A call that needs larger
+ * buffers grows them (the old ones stay allocated until kvhp_llama_destroy,
+ * so graphs captured earlier keep valid addresses); under HIP graph capture it
+ * cannot, and returns KVHP_ERR_WORKSPACE having enqueued at most the step's
+ * embedding lookup.  So: reserve before capturing decode_paged (batches up to
+ * 32; larger batches run library GEMMs, which are not meant for capture).
+ * kvhp_llama_prefill_paged / _cached synchronise and are never captured. */
+int kvhp_llama_reserve(void* model, int max_batch, int max_seq_len);
 
 #ifdef __cplusplus
 }

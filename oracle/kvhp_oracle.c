@@ -181,6 +181,36 @@ void kvo_causal_gqa_rows(const float* q, const float* k, const float* v,
     }
 }
 
+/* The rows listed in rows[0..nrows) (each in [0, S)), written to
+ * out[nrows][Hq][D]: the same attend_row arithmetic as kvo_causal_gqa_rows,
+ * for checking scattered rows of long prompts without a full-size output. */
+void kvo_causal_gqa_rowlist(const float* q, const float* k, const float* v,
+                            float* out, int64_t S, int64_t Hq, int64_t Hkv,
+                            int64_t D, const int64_t* rows, int64_t nrows,
+                            int nthreads) {
+    if (nrows <= 0) return;
+    int64_t group = Hq / Hkv;                               /* :232 */
+    float scale = 1.0f / sqrtf((float)D);                   /* :234 */
+    int64_t total = Hq * nrows;
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel num_threads(nthreads) if (nthreads > 1)
+    {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)(S > 0 ? S : 1));
+#pragma omp for schedule(dynamic, 4)
+        for (int64_t w = 0; w < total; ++w) {
+            int64_t qh = w % Hq;
+            int64_t j = w / Hq;
+            int64_t i = rows[j];
+            if (i < 0 || i >= S) continue;
+            int64_t kvh = qh / group;                       /* :240 */
+            attend_row(q + (i * Hq + qh) * D, k + kvh * D, v + kvh * D,
+                       Hkv * D, i + 1, D, scale, scores,
+                       out + (j * Hq + qh) * D);
+        }
+        free(scores);
+    }
+}
+
 void kvo_causal_gqa(const float* q, const float* k, const float* v, float* out,
                     int64_t S, int64_t Hq, int64_t Hkv, int64_t D) {
     kvo_causal_gqa_rows(q, k, v, out, S, Hq, Hkv, D, 0, S, 1);

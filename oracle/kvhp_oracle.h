@@ -55,6 +55,12 @@ void kvo_causal_gqa_rows(const float* q, const float* k, const float* v,
                          float* out, int64_t S, int64_t Hq, int64_t Hkv,
                          int64_t D, int64_t row_begin, int64_t row_end,
                          int nthreads);
+/* Rows rows[0..nrows) only (any order, each in [0,S)), output
+ * out[nrows][Hq][D]; per-row arithmetic identical to kvo_causal_gqa. */
+void kvo_causal_gqa_rowlist(const float* q, const float* k, const float* v,
+                            float* out, int64_t S, int64_t Hq, int64_t Hkv,
+                            int64_t D, const int64_t* rows, int64_t nrows,
+                            int nthreads);
 
 /* Decode: one query per sequence over its first seq_lens[b] cached keys.
  * q [B][Hq][D]; k/v contiguous [B][Hkv][cap][D]; out [B][Hq][D].

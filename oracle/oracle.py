@@ -23,6 +23,7 @@ _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
 _flt = ctypes.c_float
@@ -35,6 +36,8 @@ _ORACLE_SIGS = {
     "kvo_causal_gqa": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64]),
     "kvo_causal_gqa_rows": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64,
                                    _i64, _int]),
+    "kvo_causal_gqa_rowlist": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
+                                      _i64p, _i64, _int]),
     "kvo_decode_attention": (None, [_f32p, _f32p, _f32p, _i32p, _f32p, _i64, _i64, _i64, _i64,
                                     _i64, _int]),
     "kvo_decode_split_partial": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64,
@@ -125,6 +128,18 @@ def causal_gqa(q, k, v, hq, hkv, d, rows: Optional[tuple] = None, nthreads: int 
     out = np.zeros(q.shape, np.float32)
     rb, re = (0, s) if rows is None else rows
     lib().kvo_causal_gqa_rows(q, k, v, out, s, hq, hkv, d, rb, re, nthreads)
+    return out
+
+
+def causal_gqa_rowlist(q, k, v, hq, hkv, d, rows, nthreads: int = 1):
+    """Rows `rows` (a list of indices) of causal_gqa -> out [len(rows)][Hq][D]."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    s = q.size // (hq * d)
+    r = _c(rows, np.int64).ravel()
+    if r.size and (r.min() < 0 or r.max() >= s):
+        raise ValueError("causal_gqa_rowlist: row outside [0, S)")
+    out = np.zeros((r.size, hq, d), np.float32)
+    lib().kvo_causal_gqa_rowlist(q, k, v, out, s, hq, hkv, d, r, r.size, nthreads)
     return out
 
 

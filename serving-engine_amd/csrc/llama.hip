@@ -127,19 +127,26 @@ int alloc_n(Model& m, size_t n, T** out) {
         if (rc_) return rc_;      \
     } while (0)
 
-// Replace the model-owned buffer *p (of *cap elements) by one of n elements
-// once the stream's earlier work is done.  On failure *p is null and *cap 0.
+// Replace the model-owned buffer *p (of *cap elements) by one of at least n
+// elements (twice the old size at least, so a model retires few buffers).
+// The retired buffer stays allocated until kvhp_llama_destroy: a HIP graph
+// that captured an earlier call keeps valid addresses, and nothing has to
+// wait for the stream.  While `s` is capturing a graph nothing is allocated
+// (the allocation cannot be captured): KVHP_ERR_WORKSPACE, so size the
+// buffers first with kvhp_llama_reserve (or one eager call of the largest
+// shape).  On failure *p and *cap are unchanged.
 template <typename T>
-int regrow(Model& m, T** p, size_t* cap, size_t n, hipStream_t s) {
-    KVHP_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(regrow)");
-    if (*p) {
-        for (auto& a : m.allocs)
-            if (a == *p) a = nullptr;
-        (void)hipFree(*p);
-        *p = nullptr;
-    }
-    *cap = 0;
-    KVHP_TRY(alloc_n(m, n, p));
+int regrow(Model& m, T** p, size_t* cap, size_t n, hipStream_t s, const char* what) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    KVHP_HIP(hipStreamIsCapturing(s, &st), "hipStreamIsCapturing(regrow)");
+    KVHP_REQUIRE(st == hipStreamCaptureStatusNone, KVHP_ERR_WORKSPACE,
+                 "%s: the model's buffer must grow from %zu to %zu elements, which cannot happen "
+                 "under graph capture (call kvhp_llama_reserve before capturing)",
+                 what, *cap, n);
+    if (n < 2 * *cap) n = 2 * *cap;
+    T* fresh = nullptr;
+    KVHP_TRY(alloc_n(m, n, &fresh));
+    *p = fresh;
     *cap = n;
     return KVHP_OK;
 }
@@ -153,7 +160,7 @@ int rows_workspace(Model& m, int B, int max_seq_len, hipStream_t s, void** ws, s
                                                     max_seq_len, 0);
     if (need > m.ws_rows_bytes) {
         char* p = static_cast<char*>(m.ws_rows);
-        KVHP_TRY(regrow(m, &p, &m.ws_rows_bytes, need, s));
+        KVHP_TRY(regrow(m, &p, &m.ws_rows_bytes, need, s, "decode-attention workspace"));
         m.ws_rows = p;
     }
     *ws = m.ws_rows;
@@ -295,7 +302,8 @@ struct SuffixRows {
 int suffix_rows(Model& m, const Pages& pg, const int32_t* write_bt, int first, int rows,
                 hipStream_t s, SuffixRows& out) {
     const size_t words = 2 * (size_t)rows * pg.max_pages + 2 * (size_t)rows + 1;
-    if (m.aux_words < words) KVHP_TRY(regrow(m, &m.aux, &m.aux_words, words, s));
+    if (m.aux_words < words)
+        KVHP_TRY(regrow(m, &m.aux, &m.aux_words, words, s, "suffix block tables"));
     out.tables = m.aux;
     out.wtables = out.tables + (size_t)rows * pg.max_pages;
     out.lens = out.wtables + (size_t)rows * pg.max_pages;
@@ -400,7 +408,8 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
         const size_t part_need = kvhp_gemv_rows_workspace_bytes(H, F, B);
         if (part_need > m.part_rows_bytes) {
             char* p = static_cast<char*>(m.part_rows);
-            KVHP_TRY(regrow(m, &p, &m.part_rows_bytes, part_need, static_cast<hipStream_t>(s)));
+            KVHP_TRY(regrow(m, &p, &m.part_rows_bytes, part_need, static_cast<hipStream_t>(s),
+                            "down-projection partials"));
             m.part_rows = p;
         }
         for (int l = 0; l < c.num_layers; ++l) {
@@ -797,6 +806,45 @@ extern "C" int kvhp_llama_decode_paged(void* model, const int32_t* tokens, int b
     const Pages pg{static_cast<f16*>(pool), num_pages, block_tables, max_pages};
     return decode_rows(m, tokens, batch, pg, positions, seq_lens, max_seq_len, logits, next_tokens,
                        s);
+}
+
+extern "C" int kvhp_llama_reserve(void* model, int max_batch, int max_seq_len) {
+    clear_error();
+    KVHP_REQUIRE(model && max_batch > 0 && max_seq_len > 0, KVHP_ERR_INVALID,
+                 "llama_reserve: bad arguments");
+    Model& m = *static_cast<Model*>(model);
+    KVHP_REQUIRE(max_batch <= m.max_ctx, KVHP_ERR_INVALID,
+                 "llama_reserve: batch %d outside 1..%d", max_batch, m.max_ctx);
+    const kvhp_llama_config& c = m.c;
+    // The auto split plan depends on both the batch and the longest length,
+    // not monotonically (a grid cap per batch): take the largest workspace
+    // over every batch and every length up to the limits (lengths in 64-key
+    // steps, where the plan's chunk rounding changes, plus the limit itself).
+    size_t ws_need = 0, part_need = 0;
+    for (int b = 1; b <= max_batch; ++b) {
+        for (int len = 64;; len += 64) {
+            const int l = len < max_seq_len ? len : max_seq_len;
+            const size_t w = kvhp_decode_workspace_bytes(b, c.num_q_heads, c.num_kv_heads,
+                                                         c.head_dim, l, 0);
+            if (w > ws_need) ws_need = w;
+            if (l == max_seq_len) break;
+        }
+        if (b <= 32 && m.rows_ok) {
+            const size_t pn = kvhp_gemv_rows_workspace_bytes(c.hidden_size, c.ffn_size, b);
+            if (pn > part_need) part_need = pn;
+        }
+    }
+    if (ws_need > m.ws_rows_bytes) {
+        char* p = static_cast<char*>(m.ws_rows);
+        KVHP_TRY(regrow(m, &p, &m.ws_rows_bytes, ws_need, nullptr, "llama_reserve"));
+        m.ws_rows = p;
+    }
+    if (part_need > m.part_rows_bytes) {
+        char* p = static_cast<char*>(m.part_rows);
+        KVHP_TRY(regrow(m, &p, &m.part_rows_bytes, part_need, nullptr, "llama_reserve"));
+        m.part_rows = p;
+    }
+    return KVHP_OK;
 }
 
 extern "C" int kvhp_llama_tensor(void* model, int layer, int which, void** ptr, size_t* count) {

@@ -61,6 +61,14 @@ inline void decode_gqa(const half* q, const half* k_cache, const half* v_cache, 
 // kSplitBufferSplits splits are used (the reference accepted the buffer but
 // never used it, decode_attention_split.cu:183-214).  A sequence with
 // seq_lens[b] <= 0 gets zeros (the reference leaves its rows unwritten).
+// One-stream rule: with split_buffer == nullptr every call on a device
+// shares that device's one library workspace, so calls on two streams that
+// can overlap race on the split partials (the reference's single-stream use
+// is safe); give each stream its own split_buffer (or decode_gqa_split_ex
+// workspace) when decoding concurrently.  The workspace also grows by
+// reallocating, so a call that needs more than any earlier one must not be
+// under graph capture (decode_gqa_split_ex with a caller workspace never
+// allocates).
 inline void decode_gqa_split(const half* q, KVView k_view, KVView v_view, const int* seq_lens,
                              half* out, int batch_size, int num_q_heads, int num_kv_heads,
                              int head_dim, int max_seq_len, float* split_buffer = nullptr,

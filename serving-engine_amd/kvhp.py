@@ -128,6 +128,7 @@ _SIGNATURES = {
                                          _vp, _vp]),
     "kvhp_llama_decode_paged": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _i32,
                                        _vp, _vp, _vp]),
+    "kvhp_llama_reserve": (_i32, [_vp, _i32, _i32]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -585,6 +586,11 @@ class LlamaModel:
                                               num_pages, _ptr(block_tables), max_pages,
                                               _ptr(positions), _ptr(seq_lens), max_seq_len,
                                               _ptr(logits), _ptr(next_tokens), _stream(stream)))
+
+    def reserve(self, max_batch: int, max_seq_len: int):
+        """Size the decode buffers for every decode_paged call up to these
+        limits (required before capturing decode_paged in a HIP graph)."""
+        _check(load().kvhp_llama_reserve(self._h, max_batch, max_seq_len))
 
     def tensor(self, layer: int, which: int):
         """Host copy (numpy float16) of a model tensor."""

@@ -110,22 +110,24 @@ def test_config1_append_then_decode():
     assert_attn_close(from_gpu(out).astype(np.float32), ref, "config1")
 
 
-def test_config2_64k_split_sweep_and_invariance():
-    """BASELINE config 2 at its largest context (65536) with splits
-    {1,4,16,64}: every split count matches the oracle, and the outputs of
-    different split counts agree with each other."""
-    rng = np.random.default_rng(2)
-    hq, hkv, d, L = 32, 8, 128, 65536
+@pytest.mark.parametrize("L", [16384, 65536])
+def test_config2_split_sweep_and_invariance(L):
+    """BASELINE config 2 at its two long contexts (16384 and 65536; 4096 is
+    in test_decode_d128_splits) with splits {1,4,16,64} and the auto plan:
+    every split count matches the oracle, and the outputs of different split
+    counts agree with each other."""
+    rng = np.random.default_rng(2 if L == 65536 else 16)
+    hq, hkv, d = 32, 8, 128
     q = oracle.normal_f16(rng, (1, hq, d))
     kc, vc = oracle.normal_f16(rng, (1, hkv, L, d)), oracle.normal_f16(rng, (1, hkv, L, d))
     ref = oracle.decode_attention(q.astype(np.float32), kc.astype(np.float32),
                                   vc.astype(np.float32), np.array([L], np.int32), hq, hkv, d,
                                   nthreads=8)
     outs = []
-    for s in (1, 4, 16, 64):
-        note(f"config2 L=65536 splits={s}")
+    for s in (1, 4, 16, 64, 0):
+        note(f"config2 L={L} splits={s or 'auto'}")
         got = _run_contig(q, kc, vc, [L], hq, hkv, d, L, s)
-        assert_attn_close(got, ref, f"splits={s}")
+        assert_attn_close(got, ref, f"L={L} splits={s or 'auto'}")
         outs.append(got)
     for o in outs[1:]:
         assert np.max(np.abs(o - outs[0])) <= 2e-3

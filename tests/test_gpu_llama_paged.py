@@ -325,6 +325,92 @@ def test_paged_runner_qwen_shapes_use_the_fallback_projections():
     model.close()
 
 
+def test_decode_paged_graph_capture_needs_reserve():
+    """kvhp_llama_decode_paged under HIP graph capture: without
+    kvhp_llama_reserve its first call cannot size the model's buffers and
+    returns KVHP_ERR_WORKSPACE (nothing allocated, the capture stays valid);
+    after reserve(16, ...) a captured 16-row step (with the config-5 FFN
+    width, so the down projection's K-split partials are used) replays with
+    logits and appended K/V bit-identical to the same step run eagerly on a
+    copy of the pool -- also after eager calls in between, one of which
+    grows the buffers past the reservation (earlier buffers stay allocated,
+    so the graph's addresses stay valid)."""
+    cfg = _cfg(5632)
+    L, Hkv, D, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
+    B, plen, max_pages = 16, 9, 2
+    P = 2 * B * max_pages
+    rng = np.random.default_rng(4242)
+    pool = torch.zeros(L * 2 * Hkv * P * PAGE * D, dtype=torch.float16, device="cuda")
+    bt = torch.from_numpy(rng.permutation(P).astype(np.int32).reshape(2 * B, max_pages)).cuda()
+    model = kvhp.LlamaModel(cfg, seed=12, max_ctx=64)
+    toks = []
+    for b in range(2 * B):
+        t, _ = model.prefill_paged(rng.integers(0, V, plen).astype(np.int32), pool, P, bt[b],
+                                   max_pages)
+        toks.append(t)
+    toks = torch.tensor(toks, dtype=torch.int32, device="cuda")
+    pos = torch.full((2 * B,), plen, dtype=torch.int32, device="cuda")
+    sl = pos + 1
+    lg = torch.empty(2 * B, V, dtype=torch.float32, device="cuda")
+    nx = torch.empty(2 * B, dtype=torch.int32, device="cuda")
+    cap_len = plen + 1
+
+    def step(n, pl, out_lg, out_nx):
+        model.decode_paged(toks[:n], pl, P, bt[:n], max_pages, pos[:n], sl[:n], cap_len,
+                           out_lg[:n], out_nx[:n])
+
+    torch.cuda.synchronize()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    g0 = torch.cuda.CUDAGraph()
+    err = None
+    pool_try = pool.clone()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(cs):
+        g0.capture_begin()
+        try:
+            step(B, pool_try, lg, nx)
+        except kvhp.KVHPError as e:
+            err = e
+        finally:
+            g0.capture_end()
+    torch.cuda.current_stream().wait_stream(cs)
+    torch.cuda.synchronize()
+    del g0
+    assert err is not None and err.code == kvhp.KVHP_ERR_WORKSPACE, err
+
+    model.reserve(B, cap_len)
+    pool_g = pool.clone()
+    g = torch.cuda.CUDAGraph()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g, stream=cs):
+        step(B, pool_g, lg, nx)
+    torch.cuda.current_stream().wait_stream(cs)
+    torch.cuda.synchronize()
+    pool_e = pool.clone()
+    lg_e = torch.empty_like(lg)
+    nx_e = torch.empty_like(nx)
+    step(B, pool_e, lg_e, nx_e)              # eager reference of the captured step
+    torch.cuda.synchronize()
+    lg_ref, nx_ref, pool_ref = lg_e[:B].clone(), nx_e[:B].clone(), pool_e.clone()
+    scratch = pool.clone()
+    for i, between in enumerate((None, 4, 2 * B)):
+        if between:
+            # eager calls on another pool copy: a smaller batch (reserved), then
+            # a larger one, which grows the buffers past the reservation
+            step(between, scratch, lg_e, nx_e)
+            torch.cuda.synchronize()
+        pool_g.copy_(pool)
+        lg.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(lg[:B], lg_ref), f"replay {i}: logits differ from the eager step"
+        assert torch.equal(nx[:B], nx_ref), f"replay {i}: tokens differ"
+        assert torch.equal(pool_g, pool_ref), f"replay {i}: appended K/V differ"
+    del g
+    model.close()
+
+
 def test_paged_runner_argument_errors():
     cfg = _cfg()
     model = kvhp.LlamaModel(cfg, seed=3, max_ctx=32)

@@ -70,6 +70,22 @@ def test_causal_bit_exact_vs_reference_build(s, hq, hkv, d):
     assert np.array_equal(ours.view(np.uint32), ref.view(np.uint32))
 
 
+def test_causal_rowlist_equals_full_rows():
+    """causal_gqa_rowlist (scattered rows of long prompts) returns exactly the
+    listed rows of the full causal_gqa, in the listed order, with repeats;
+    out-of-range rows are refused."""
+    rng = np.random.default_rng(90)
+    s, hq, hkv, d = 97, 8, 2, 64
+    q, k, v = f16(rng, (s, hq, d)), f16(rng, (s, hkv, d)), f16(rng, (s, hkv, d))
+    full = oracle.causal_gqa(q, k, v, hq, hkv, d)
+    rows = [96, 0, 31, 32, 63, 64, 5, 5, 95]
+    got = oracle.causal_gqa_rowlist(q, k, v, hq, hkv, d, rows, nthreads=3)
+    assert np.array_equal(got.view(np.uint32), full[rows].view(np.uint32))
+    assert oracle.causal_gqa_rowlist(q, k, v, hq, hkv, d, []).shape == (0, hq, d)
+    with pytest.raises(ValueError):
+        oracle.causal_gqa_rowlist(q, k, v, hq, hkv, d, [s])
+
+
 def _golden():
     return np.load(GOLDEN, allow_pickle=False)
 

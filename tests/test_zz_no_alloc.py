@@ -91,3 +91,68 @@ def test_noalloc_refuses_plans_beyond_the_scratch():
     assert e.value.code == kvhp.KVHP_ERR_WORKSPACE, e.value
     assert "static scratch" in str(e.value)
     sync()
+
+
+def _pool_only(rng, lens, hq, hkv, d):
+    """A random fp16 pool and seeded page tables on the GPU (no oracle)."""
+    lens = np.asarray(lens, np.int32)
+    bt, P = make_block_tables(rng, lens)
+    gen = torch.Generator(device="cuda").manual_seed(int(rng.integers(1 << 30)))
+    pk = torch.randn((hkv, P, 16, d), generator=gen, device="cuda").half()
+    pv = torch.randn((hkv, P, 16, d), generator=gen, device="cuda").half()
+    bt_t = to_gpu(bt)
+    q = torch.empty((lens.size, hq, d), dtype=torch.float16, device="cuda")
+    return q, (kvhp.paged_view(pk, bt_t), kvhp.paged_view(pv, bt_t)), to_gpu(lens), (pk, pv, bt_t)
+
+
+def test_noalloc_captured_in_a_graph_replays_bit_exact():
+    """Two noalloc calls captured in one HIP graph on a side stream -- a
+    32-sequence batch on the device-balanced plan (D=128, auto splits) and a
+    4-sequence batch with 4 fixed splits (32/4 heads of 64) -- sharing the
+    static scratch one after the other.  The first call on a device resolves
+    the scratch address and its kernels' occupancy, so one eager call of each
+    runs first (the header asks for that).  Three replays, each with new q
+    values and eager work and a synchronisation in between: every replay's
+    outputs equal kvhp_decode_attention run eagerly on the same inputs, bit
+    for bit."""
+    rng = np.random.default_rng(2027)
+    lens_a = rng.integers(128, 4097, size=32).astype(np.int32)
+    lens_b = np.array([700, 33, 0, 2000], np.int32)
+    cases = [(_pool_only(rng, lens_a, 32, 8, 128), 32, 8, 128, int(lens_a.max()), 0),
+             (_pool_only(rng, lens_b, 32, 4, 64), 32, 4, 64, int(lens_b.max()), 4)]
+    outs = [torch.full((c[0][0].shape[0], c[1], c[3]), float("nan"), dtype=torch.float16,
+                       device="cuda") for c in cases]
+
+    def run_noalloc():
+        for ((q, views, lt, _), hq, hkv, d, ml, sp), o in zip(cases, outs):
+            kvhp.decode_attention_noalloc(q, views[0], views[1], lt, o, hq, hkv, d, ml, sp)
+
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    for (q, _, _, _), *_ in cases:
+        q.copy_(torch.randn(q.shape, generator=gen, device="cuda").half())
+    note("noalloc graph: eager first calls")
+    run_noalloc()
+    sync()
+    g = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    note("noalloc graph: capture")
+    with torch.cuda.graph(g, stream=cs):
+        run_noalloc()
+    torch.cuda.current_stream().wait_stream(cs)
+    sync()
+    for r in range(3):
+        for (q, _, _, _), *_ in cases:
+            q.copy_(torch.randn(q.shape, generator=gen, device="cuda").half())
+        for o in outs:
+            o.fill_(float("nan"))
+        note(f"noalloc graph: replay {r}")
+        g.replay()
+        sync()
+        for i, (((q, views, lt, _), hq, hkv, d, ml, sp), o) in enumerate(zip(cases, outs)):
+            want = torch.full_like(o, float("nan"))
+            kvhp.decode_attention(q, views[0], views[1], lt, want, hq, hkv, d, ml, sp)
+            sync()
+            assert np.array_equal(from_gpu(o).view(np.uint16), from_gpu(want).view(np.uint16)), \
+                f"replay {r}, call {i}: graph output differs from the eager call"
+    del g
