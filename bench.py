@@ -70,14 +70,16 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5,c5b,kv")
     ap.add_argument("--profile", nargs="?", const="decode", default=None,
-                    choices=("decode", "prefill", "c5", "batched", "c2"),
+                    choices=("decode", "prefill", "c5", "batched", "c2", "kv"),
                     help="short run for rocprofv3: a 256 MiB device copy (counter "
                          "calibration) then the config-3 steps (decode), config-4 "
                          "S=2048 prefill calls (prefill), --steps config-5 decode "
                          "steps without the HIP graph (c5), --steps batched decode "
                          "steps of the config-5 model at B = 1, 8, 32 (batched) or "
                          "--steps flushed config-2 calls (auto splits) per context "
-                         "(c2); no CPU baseline, no extras")
+                         "(c2), or the KV movement kernels: paged gather and 2048-token "
+                         "appends, flushed and rotating over copies (kv); no CPU "
+                         "baseline, no extras")
     return ap.parse_args()
 
 
@@ -500,30 +502,100 @@ def run_kv_movement(torch, kvhp):
     g_write = b * hkv * cap * d * 2 * 2
     del ok, ov, c
     torch.cuda.empty_cache()
-    S, hkv2, d2 = 2048, 8, 128
-    src_k = torch.randn((1, S, hkv2, d2), device="cuda").half()
-    src_v = torch.randn_like(src_k)
-    P = S // 16 + 4
-    pk = torch.zeros((hkv2, P, 16, d2), dtype=torch.float16, device="cuda")
-    pv = torch.zeros_like(pk)
-    bt = torch.arange(P, dtype=torch.int32, device="cuda").view(1, P)
-    zero = torch.zeros(1, dtype=torch.int32, device="cuda")
-    a_p = time_op(torch, lambda: kvhp.paged_append_kv(src_k, src_v, pk, pv, bt, zero, 1, S, hkv2,
-                                                      d2), 20, fl)[0]
-    ck = torch.zeros((hkv2, S, d2), dtype=torch.float16, device="cuda")
-    cv = torch.zeros_like(ck)
-    a_c = time_op(torch, lambda: kvhp.append_kv(src_k, src_v, ck, cv, S, 0, hkv2, S, d2), 20, fl)[0]
-    a_bytes = 2 * S * hkv2 * d2 * 2 * 2
+    hkv2, d2 = 8, 128
+
+    def rotating(fn, R, rounds=3):
+        """us per call, calls back to back over R input/output copies: R calls
+        captured as one HIP graph (eager launches from Python are host-bound
+        at these sizes), replayed `rounds` times under HIP events."""
+        for i in range(R):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        cs = torch.cuda.Stream()
+        cs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.graph(g, stream=cs):
+            for i in range(R):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(cs)
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(rounds):
+            g.replay()
+        e1.record()
+        e1.synchronize()
+        del g
+        return e0.elapsed_time(e1) * 1e3 / (rounds * R)
+
+    def append_case(S, flushed):
+        """Appends of S tokens x 8 heads x D=128 (K and V), paged (identity
+        table from position 0) and contiguous, over R copies totalling more
+        than the 256 MB MALL; beside them torch's device copy of the same
+        bytes (src -> dst, K and V): the ceiling of a plain copy that size."""
+        nb = 2 * S * hkv2 * d2 * 2 * 2
+        R = max(3, -(-640_000_000 // nb))
+        P = S // 16 + 4
+        bt = torch.arange(P, dtype=torch.int32, device="cuda").view(1, P)
+        zero = torch.zeros(1, dtype=torch.int32, device="cuda")
+        srcs = [(torch.randn((1, S, hkv2, d2), device="cuda").half(),
+                 torch.randn((1, S, hkv2, d2), device="cuda").half()) for _ in range(R)]
+        pools = [(torch.zeros((hkv2, P, 16, d2), dtype=torch.float16, device="cuda"),
+                  torch.zeros((hkv2, P, 16, d2), dtype=torch.float16, device="cuda"))
+                 for _ in range(R)]
+        caches = [(torch.zeros((hkv2, S, d2), dtype=torch.float16, device="cuda"),
+                   torch.zeros((hkv2, S, d2), dtype=torch.float16, device="cuda"))
+                  for _ in range(R)]
+
+        def paged(i):
+            kvhp.paged_append_kv(srcs[i][0], srcs[i][1], pools[i][0], pools[i][1], bt, zero, 1,
+                                 S, hkv2, d2)
+
+        def contig(i):
+            kvhp.append_kv(srcs[i][0], srcs[i][1], caches[i][0], caches[i][1], S, 0, hkv2, S,
+                           d2)
+
+        def copy(i):
+            caches[i][0].view(-1).copy_(srcs[i][0].view(-1))
+            caches[i][1].view(-1).copy_(srcs[i][1].view(-1))
+
+        row = {"tokens": S, "bytes": nb, "copies": R}
+        for name, fn in (("paged", paged), ("contig", contig), ("torch_copy", copy)):
+            us = rotating(fn, R)
+            row[name] = {"us": round(us, 2), "GBps": round(nb / us / 1e3, 1)}
+        if flushed:
+            for name, fn in (("paged", paged), ("contig", contig)):
+                t = time_op(torch, lambda: fn(0), 20, fl)[0]
+                row[name]["flushed_us"] = round(t, 2)
+                row[name]["flushed_GBps"] = round(nb / t / 1e3, 1)
+        del srcs, pools, caches
+        torch.cuda.empty_cache()
+        return row
+
+    a2048 = append_case(2048, True)
+    sweep = [append_case(S, False) for S in (8192, 32768)]
+    del fl
+    torch.cuda.empty_cache()
+    a_bytes = a2048["bytes"]
     return {"workload": "paged gather of the config-3 pool (32 seqs, sum L=%d) into contiguous "
-                        "K/V [32][8][%d][128]; append of 2048 tokens x 8 heads x D=128" % (
-                            int(L1.sum()), cap),
+                        "K/V [32][8][%d][128]; append of 2048 tokens x 8 heads x D=128 (and "
+                        "8192 / 32768 tokens as a size sweep)" % (int(L1.sum()), cap),
             "gather_us": round(g, 2), "gather_us_min": round(gt[2], 2),
             "gather_us_max": round(gt[3], 2), "gather_bytes": g_read + g_write,
             "gather_GBps": round((g_read + g_write) / g / 1e3, 1),
-            "paged_append_2048_us": round(a_p, 2),
-            "contig_append_2048_us": round(a_c, 2), "append_bytes": a_bytes,
-            "paged_append_GBps": round(a_bytes / a_p / 1e3, 1),
-            "contig_append_GBps": round(a_bytes / a_c / 1e3, 1)}
+            "paged_append_2048_us": a2048["paged"]["flushed_us"],
+            "contig_append_2048_us": a2048["contig"]["flushed_us"], "append_bytes": a_bytes,
+            "paged_append_GBps": a2048["paged"]["flushed_GBps"],
+            "contig_append_GBps": a2048["contig"]["flushed_GBps"],
+            "append_2048": a2048, "append_sweep": sweep,
+            "note": "*_append_2048_us: one call after a cache flush, HIP events around it "
+                    "(median of 20; includes the launch); append_2048 / append_sweep: calls "
+                    "back to back over separately allocated input/output copies (more than "
+                    "the 256 MB MALL in all), replayed from one HIP graph, HIP events around "
+                    "3 replays; torch_copy = a plain device copy of the same bytes (the "
+                    "ceiling of a copy that size)"}
 
 
 def run_config1(torch, kvhp):
@@ -927,6 +999,9 @@ def main():
         if args.profile == "batched":
             rb = run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=args.steps)
             print(json.dumps({"profile": "batched", "config5_batched": rb}))
+            return
+        if args.profile == "kv":
+            print(json.dumps({"profile": "kv", "kv_movement": run_kv_movement(torch, kvhp)}))
             return
     log("stream-read ceiling ...")
     sr = run_stream_read(torch, kvhp)

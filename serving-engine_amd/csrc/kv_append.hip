@@ -1,9 +1,11 @@
 // kv_append.hip -- KV-cache writes and the paged gather (bit-exact copies).
 //
-// Layout: every kernel moves 16-byte vectors (8 fp16).  One work item is one
-// 16-byte chunk of a K row plus the same chunk of the V row, so a wave copies
-// 1 KiB of K and 1 KiB of V per step with fully coalesced, 16-byte aligned
-// accesses; the token-major source [T][Hkv][D] is read in address order.
+// Layout: every kernel moves 16-byte vectors (8 fp16).  Appends of 16 or
+// more tokens go by runs (one wave per 16 tokens of one KV head: a page's
+// worth of rows, all loads before the stores); shorter ones and the generic
+// gather by chunks (one work item is one 16-byte chunk of a K row plus the
+// same chunk of the V row, fully coalesced, 16-byte aligned); the paged
+// gather by pages.
 // These kernels are HBM-bound byte copies: algorithmic traffic is exactly
 // 2 (read+write) x 2 (K,V) x T*Hkv*D*2 bytes (+4 B per block-table lookup).
 // A scalar (2-byte) variant handles head dims that are not multiples of 8.
@@ -81,6 +83,114 @@ append_paged_kernel(const f16* __restrict__ src_k, const f16* __restrict__ src_v
             pool_k[dofs] = src_k[so];
             pool_v[dofs] = src_v[so];
         }
+    }
+}
+
+// Append by runs (prompt-sized T): one wave moves a run of 16 consecutive
+// tokens of one KV head, K and V.  The run's source rows are D-element
+// pieces of the token-major [B][T][Hkv][D] input (row pitch Hkv*D); they land
+// as 16 consecutive rows of the destination -- one 32*D-byte page when the
+// run starts on a page boundary (prefill from position 0), two pages
+// otherwise, or 16 consecutive rows of the head-major contiguous cache.
+// CPL = D/32 16-byte chunks per lane and tensor, every load of the run in
+// flight before its stores; unit indices and row/column splits are 32-bit
+// shifts and masks (no 64-bit division per chunk).  Units run KV head
+// fastest, so a workgroup's four waves read the same tokens' rows.  Each
+// destination row is written by exactly the lanes that loaded it, with the
+// same drop rules as the chunk kernels: positions >= max_seq (contiguous),
+// or negative, past max_pages, or whose page id lies outside the pool
+// (paged).
+template <int CPL, bool PAGED>
+__global__ void __launch_bounds__(kCopyThreads)
+append_runs_kernel(const f16* __restrict__ src_k, const f16* __restrict__ src_v,
+                   f16* __restrict__ dst_k, f16* __restrict__ dst_v,
+                   const int32_t* __restrict__ block_tables, int max_pages,
+                   const int32_t* __restrict__ start_pos_dev, int start_pos, int num_units,
+                   int runs_per_seq, int num_tokens, int num_kv_heads, int max_seq,
+                   int num_pages) {
+    constexpr int D = 32 * CPL;
+    constexpr int CPR = D / 8;                        // 16-byte chunks per row
+    constexpr int RSH = CPR == 4 ? 2 : CPR == 8 ? 3 : CPR == 16 ? 4 : 5;
+    static_assert((1 << RSH) == CPR, "chunks per row must be 4..32");
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nwaves = static_cast<int>(((int64_t)gridDim.x * blockDim.x) >> 6);
+    for (int u = static_cast<int>(((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+         u < num_units; u += nwaves) {
+        const int h = u % num_kv_heads;
+        const int br = u / num_kv_heads;              // b * runs_per_seq + r
+        const int b = br / runs_per_seq;
+        const int t0 = kPage * (br - b * runs_per_seq);
+        const int p0 = (PAGED ? start_pos_dev[b] : start_pos) + t0;
+        int64_t so[CPL], dofs[CPL];
+        bool ok[CPL];
+        half8 kx[CPL], vx[CPL];
+        // The source loads depend on the token index only; the destination's
+        // page id is loaded alongside them and checked at the store, so the
+        // K/V loads never wait for the block table.
+        int pid[CPL];
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + kWave * i;
+            const int row = c >> RSH;
+            const int col = c & (CPR - 1);
+            const int t = t0 + row;
+            const int pos = p0 + row;
+            const bool src_ok = t < num_tokens;
+            bool v = src_ok && pos >= 0;
+            pid[i] = -1;
+            if constexpr (PAGED) {
+                const int pi = pos >> 4;
+                if (v && pi < max_pages) pid[i] = block_tables[(int64_t)b * max_pages + pi];
+                dofs[i] = ((int64_t)h * num_pages * kPage + (pos & (kPage - 1))) * D + 8 * col;
+            } else {
+                v = v && pos < max_seq;
+                dofs[i] = ((int64_t)h * max_seq + pos) * D + 8 * col;
+            }
+            ok[i] = v;
+            so[i] = (((int64_t)b * num_tokens + t) * num_kv_heads + h) * D + 8 * col;
+            kx[i] = src_ok ? load_half8(src_k + so[i]) : half8{};
+            vx[i] = src_ok ? load_half8(src_v + so[i]) : half8{};
+        }
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            bool v = ok[i];
+            int64_t o = dofs[i];
+            if constexpr (PAGED) {
+                v = v && pid[i] >= 0 && pid[i] < num_pages;
+                o += (int64_t)pid[i] * kPage * D;
+            }
+            if (v) {
+                store_half8(dst_k + o, kx[i]);
+                store_half8(dst_v + o, vx[i]);
+            }
+        }
+    }
+}
+
+// Launch of append_runs_kernel for D in {32, 64, 128, 256} (16-byte aligned
+// tensors); false when the shape needs the chunk kernels.
+template <bool PAGED>
+bool launch_append_runs(const void* src_k, const void* src_v, void* dst_k, void* dst_v,
+                        const int32_t* bt, int max_pages, const int32_t* start_dev,
+                        int start_host, int batch, int num_tokens, int num_kv_heads,
+                        int head_dim, int max_seq, int num_pages, hipStream_t s) {
+    const int runs = (num_tokens + kPage - 1) / kPage;
+    const int64_t units = (int64_t)batch * runs * num_kv_heads;
+    if (units > (int64_t)1 << 30) return false;
+    const int64_t blocks = std::min<int64_t>((units + 3) / 4, 256 * 64);
+    const dim3 grid(static_cast<unsigned>(std::max<int64_t>(blocks, 1)));
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(kCopyThreads), 0, s, (const f16*)src_k,
+                           (const f16*)src_v, (f16*)dst_k, (f16*)dst_v, bt, max_pages,
+                           start_dev, start_host, static_cast<int>(units), runs, num_tokens,
+                           num_kv_heads, max_seq, num_pages);
+    };
+    switch (head_dim) {
+        case 32: go(append_runs_kernel<1, PAGED>); return true;
+        case 64: go(append_runs_kernel<2, PAGED>); return true;
+        case 128: go(append_runs_kernel<4, PAGED>); return true;
+        case 256: go(append_runs_kernel<8, PAGED>); return true;
+        default: return false;
     }
 }
 
@@ -211,6 +321,13 @@ extern "C" int kvhp_append_kv(const void* src_k, const void* src_v,
     const int cpr = head_dim / vw;
     const int64_t n = (int64_t)num_tokens * num_kv_heads * cpr;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    // prompt-sized appends by 16-token runs; a few tokens by 16-byte chunks
+    // (a run of one token would leave most of a wave's lanes idle)
+    if (vec && num_tokens >= kPage &&
+        launch_append_runs<false>(src_k, src_v, dst_k_head_base, dst_v_head_base, nullptr, 0,
+                                  nullptr, start_pos, 1, num_tokens, num_kv_heads, head_dim,
+                                  max_seq, 0, s))
+        return check_launch("append_kv");
     if (vec)
         hipLaunchKernelGGL(append_contig_kernel<8>, dim3(copy_grid(n)), dim3(kCopyThreads),
                            0, s, (const f16*)src_k, (const f16*)src_v,
@@ -244,6 +361,11 @@ extern "C" int kvhp_paged_append_kv(const void* src_k, const void* src_v,
     const int cpr = head_dim / vw;
     const int64_t n = (int64_t)batch * num_tokens * num_kv_heads * cpr;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (vec && num_tokens >= kPage &&
+        launch_append_runs<true>(src_k, src_v, pool_k, pool_v, block_tables, max_pages,
+                                 start_pos, 0, batch, num_tokens, num_kv_heads, head_dim, 0,
+                                 num_pages, s))
+        return check_launch("paged_append_kv");
     if (vec)
         hipLaunchKernelGGL(append_paged_kernel<8>, dim3(copy_grid(n)), dim3(kCopyThreads),
                            0, s, (const f16*)src_k, (const f16*)src_v, (f16*)pool_k,

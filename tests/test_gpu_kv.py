@@ -89,6 +89,57 @@ def test_paged_append_drops_out_of_range():
     del torch
 
 
+@pytest.mark.parametrize("t,start,hkv,d,max_seq", [
+    (2048, 0, 8, 128, 2048), (16, 5, 4, 32, 40), (333, 31, 2, 64, 400), (100, 7, 3, 256, 120),
+    (17, 0, 1, 128, 17), (64, 48, 8, 64, 90)])
+def test_append_runs_bit_exact(t, start, hkv, d, max_seq):
+    """Appends of 16 or more tokens run by 16-token runs (one wave per run and
+    KV head): page-aligned and unaligned starts, partial last runs, every
+    vectorised head dim (32..256) and positions past max_seq dropped."""
+    import torch
+    rng = np.random.default_rng(t * 7 + start + d)
+    sk, sv = _src(rng, (t, hkv, d)), _src(rng, (t, hkv, d))
+    pre = _src(rng, (hkv, max_seq, d))
+    note(f"append runs T={t} start={start} Hkv={hkv} D={d} max_seq={max_seq}")
+    dk, dv = to_gpu_f16(pre), to_gpu_f16(pre.copy())
+    kvhp.append_kv(to_gpu_f16(sk), to_gpu_f16(sv), dk, dv, t, start, hkv, max_seq, d)
+    sync()
+    ek = pre.view(np.uint16).copy()
+    ev = pre.view(np.uint16).copy()
+    oracle.append_kv(sk.view(np.uint16), sv.view(np.uint16), ek, ev, t, start, hkv, max_seq, d)
+    assert np.array_equal(from_gpu(dk).view(np.uint16), ek)
+    assert np.array_equal(from_gpu(dv).view(np.uint16), ev)
+
+
+@pytest.mark.parametrize("t,d", [(16, 32), (50, 64), (129, 128), (40, 256)])
+def test_paged_append_runs_bit_exact(t, d):
+    """Paged appends of 16 or more tokens (runs): sequences starting on and
+    off a page boundary, a negative start (rows before position 0 dropped),
+    a run crossing into a -1 table entry and an id outside the pool
+    (dropped), and a sequence running past max_pages (dropped)."""
+    import torch
+    rng = np.random.default_rng(500 + t + d)
+    hkv, b, max_pages = 3, 5, 12
+    start = np.array([0, 9, -5, 16 * max_pages - t // 2, 33], np.int32)
+    P = b * max_pages
+    bt = rng.permutation(P).astype(np.int32).reshape(b, max_pages)
+    bt[1, (9 + t // 2) // 16] = -1
+    bt[4, 2] = P + 3
+    sk, sv = _src(rng, (b, t, hkv, d)), _src(rng, (b, t, hkv, d))
+    pool0 = _src(rng, (hkv, P, 16, d))
+    note(f"paged append runs T={t} D={d}")
+    pk, pv = to_gpu_f16(pool0), to_gpu_f16(pool0.copy())
+    kvhp.paged_append_kv(to_gpu_f16(sk), to_gpu_f16(sv), pk, pv, to_gpu(bt), to_gpu(start),
+                         b, t, hkv, d)
+    sync()
+    ek = pool0.view(np.uint16).copy()
+    ev = pool0.view(np.uint16).copy()
+    oracle.paged_append(sk.view(np.uint16), sv.view(np.uint16), ek, ev, bt, start, b, t, hkv, d)
+    assert np.array_equal(from_gpu(pk).view(np.uint16), ek)
+    assert np.array_equal(from_gpu(pv).view(np.uint16), ev)
+    del torch
+
+
 @pytest.mark.parametrize("b,hkv,d,maxlen", [(3, 2, 64, 100), (8, 8, 128, 700), (2, 1, 40, 33),
                                             (4, 3, 32, 50), (2, 2, 256, 90)])
 def test_paged_gather_bit_exact(b, hkv, d, maxlen):
