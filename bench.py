@@ -68,7 +68,8 @@ def parse():
                          "over (504 MB each)")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 2 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of extra parts: c1,c2,c4,c5,c5b,kv")
+    ap.add_argument("--only", default="",
+                    help="comma list of extra parts: c1,c2,c4,c5,c5b,kv,layout")
     ap.add_argument("--profile", nargs="?", const="decode", default=None,
                     choices=("decode", "prefill", "c5", "batched", "c2", "kv"),
                     help="short run for rocprofv3: a 256 MiB device copy (counter "
@@ -125,14 +126,16 @@ def spread(t, nbytes=None):
     return d
 
 
-def run_page_read(torch, kvhp, nbytes, page_bytes=4096, reps=25):
+def run_page_read(torch, kvhp, nbytes, page_bytes=4096, reps=25, ordered=False):
     """Ceiling of a paged decode's page reads (kvhp_page_read): a dense pool of
-    nbytes read once in a seeded random page order, as the config-3 step
-    reads its pool; flushed before each rep, 5 warm-up and `reps` timed reps."""
+    nbytes read once in a seeded random page order (ordered: address order),
+    as the config-3 step reads its pool; flushed before each rep, 5 warm-up
+    and `reps` timed reps."""
     n = max(1, nbytes // page_bytes)
     pool = torch.ones((n * page_bytes) // 4, dtype=torch.float32, device="cuda")
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
-    ids = torch.from_numpy(np.random.default_rng(7).permutation(n).astype(np.int32)).cuda()
+    order = np.arange(n) if ordered else np.random.default_rng(7).permutation(n)
+    ids = torch.from_numpy(order.astype(np.int32)).cuda()
     fl = Flusher(torch)
     for _ in range(5):
         kvhp.page_read(pool, ids, page_bytes, sink)
@@ -144,8 +147,62 @@ def run_page_read(torch, kvhp, nbytes, page_bytes=4096, reps=25):
             "GBps_worst": round(rb / t[3] / 1e3, 1), "bytes": rb, "pages": n,
             "page_bytes": page_bytes, "reps": reps,
             "pct_of_spec": round(rb / t[0] / 1e3 / HBM_PEAK_GBS * 100, 1),
-            "kernel": "page_read_kernel (kvhp_page_read), dense pool in random page order, "
-                      "flushed"}
+            "kernel": "page_read_kernel (kvhp_page_read), dense pool in %s page order, "
+                      "flushed" % ("address" if ordered else "random")}
+
+
+def run_page_layout(torch, kvhp, reps=20):
+    """Is the config-3 step's ceiling the page layout's?  (1) The page-read
+    ceiling at the decode's bytes for pages of 2 to 32 KB in random order, and
+    4 KB pages in address order; (2) the config-3 step (fused append +
+    decode, flushed single calls) with the config's random page tables and
+    with each sequence's pages in address order, timed alternately."""
+    c = build_config3(torch, kvhp)
+    b, hq, hkv, d = c["b"], c["hq"], c["hkv"], c["d"]
+    L1 = c["lens"] + 1
+    dbytes = decode_bytes(L1, hq, hkv, d)
+    del c
+    torch.cuda.empty_cache()
+    sweep = []
+    for pb in (2048, 4096, 8192, 16384, 32768):
+        r = run_page_read(torch, kvhp, dbytes, pb, reps)
+        sweep.append({"page_bytes": pb, "GBps": r["GBps"], "GBps_best": r["GBps_best"]})
+    r = run_page_read(torch, kvhp, dbytes, 4096, reps, ordered=True)
+    addr = {"page_bytes": 4096, "GBps": r["GBps"], "GBps_best": r["GBps_best"]}
+    max_len = int(L1.max())
+    ws_bytes = kvhp.decode_workspace_bytes(b, hq, hkv, d, max_len, 0)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device="cuda")
+    kvhp.decode_workspace_init(ws)
+    fl = Flusher(torch)
+    steps = {}
+    for name, ordered in (("random", False), ("address", True)):
+        ci = build_config3(torch, kvhp, ordered=ordered)
+        kv, vv = kvhp.paged_view(ci["pool_k"], ci["bt"]), kvhp.paged_view(ci["pool_v"], ci["bt"])
+        nk, nv = ci["new_k"].view(b, hkv, d), ci["new_v"].view(b, hkv, d)
+
+        def fn(ci=ci, kv=kv, vv=vv, nk=nk, nv=nv):
+            kvhp.paged_append_decode(ci["q"], nk, nv, kv, vv, ci["pos"], ci["lens1"], ci["out"],
+                                     hq, hkv, d, max_len, 0, ws)
+        for _ in range(3):
+            fn()
+        steps[name] = (ci, fn, [])
+    for _ in range(3):
+        for name in ("random", "address"):
+            steps[name][2].append(time_op(torch, steps[name][1], reps // 3 + 1, fl)[0])
+    sbytes = dbytes + append_bytes(b, hkv, d)
+    res = {}
+    for name in ("random", "address"):
+        us = float(np.median(steps[name][2]))
+        res[name] = {"us": round(us, 2), "GBps": round(sbytes / us / 1e3, 1),
+                     "frac": round(sbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "us_runs": [round(x, 2) for x in steps[name][2]]}
+    del steps, fl, ws
+    torch.cuda.empty_cache()
+    return {"workload": "config-3 decode bytes (%d B): page-read ceiling by page size (random "
+                        "order) and in address order; the config-3 step (kvhp_paged_append_decode, "
+                        "flushed single calls, median of 3 alternating runs) with random and "
+                        "address-ordered page tables" % dbytes,
+            "page_read_random": sweep, "page_read_address_4k": addr, "step": res}
 
 
 def run_stream_read(torch, kvhp, gib=2, reps=25):
@@ -182,9 +239,11 @@ def append_bytes(b, hkv, d):
     return b * hkv * d * 2 * 2 * 2 + b * 4 * 2
 
 
-def build_config3(torch, kvhp, seed=3, value_seed=None):
+def build_config3(torch, kvhp, seed=3, value_seed=None, ordered=False):
     """Config-3 inputs: lengths and page tables from numpy seed `seed`, K/V
-    pool, new rows and q from torch seed `value_seed` (default `seed`)."""
+    pool, new rows and q from torch seed `value_seed` (default `seed`).
+    ordered: page ids dealt in address order (each sequence's pages
+    contiguous in the pool) instead of the config's random permutation."""
     b, hq, hkv, d = 32, 32, 8, 128
     rng = np.random.default_rng(seed)
     lens = rng.integers(128, 8193, size=b).astype(np.int32)  # cached tokens
@@ -192,6 +251,8 @@ def build_config3(torch, kvhp, seed=3, value_seed=None):
     P = int(need.sum()) + 16
     maxp = int(need.max()) + 1
     perm = rng.permutation(P).astype(np.int32)
+    if ordered:
+        perm = np.arange(P, dtype=np.int32)
     bt = np.full((b, maxp), -1, np.int32)
     o = 0
     for i, n in enumerate(need):
@@ -864,15 +925,18 @@ def run_config5_eager(torch, kvhp, steps=32, prompt_len=2048):
             "first_tokens": toks[:8].tolist()}
 
 
-def run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=20, ctx=2048):
+def run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=20, ctx=2048, rounds=3):
     """The config-5 model serving B sequences at once through the batched
     runner (kvhp_llama_decode_paged: caller-owned page pool, one block-table
-    row per sequence, eager launches): every sequence prefilled with a
-    seeded ctx-id prompt, then `steps` timed decode steps per batch size."""
+    row per sequence): every sequence prefilled with a seeded ctx-id prompt,
+    then `steps` decode steps per batch size, launched eagerly and replayed
+    from one HIP graph of the same steps (same positions and lengths in
+    device memory, same attention plan), the two timed alternately `rounds`
+    times; the graph's last logits must equal an eager step's bit for bit."""
     cfg = kvhp.llama_1b_config()
     L, hkv, d, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
     bmax = max(batches)
-    per = (ctx + 3 * steps + 24 + 15) // 16   # eager steps, then the graph's
+    per = (ctx + steps + 15) // 16
     P = bmax * per
     model = kvhp.LlamaModel(cfg, seed=5, max_ctx=max(ctx, bmax))
     pool = torch.zeros(L * 2 * hkv * P * 16 * d, dtype=torch.float16, device="cuda")
@@ -882,70 +946,72 @@ def run_config5_batched(torch, kvhp, batches=(1, 8, 32), steps=20, ctx=2048):
              for b in range(bmax)]
     logits = torch.empty(bmax, V, dtype=torch.float32, device="cuda")
     nxt = torch.empty(bmax, dtype=torch.int32, device="cuda")
+    # step i writes position ctx + i of every row and attends over ctx + i + 1
+    # keys; every run of the steps rewrites the same K/V (same tokens)
+    pos_all = (ctx + torch.arange(steps, dtype=torch.int32, device="cuda")).view(steps, 1)
+    cap_len = ctx + steps
+    model.reserve(bmax, cap_len)
     out = {}
+    ev = lambda: torch.cuda.Event(enable_timing=True)
     for B in batches:
         toks = torch.tensor(first[:B], dtype=torch.int32, device="cuda")
+        pos_b = pos_all.expand(steps, B).contiguous()
+        seq_b = pos_b + 1
 
-        def step(pos):
-            p = torch.full((B,), pos, dtype=torch.int32, device="cuda")
-            model.decode_paged(toks, pool, P, bt[:B], per, p, p + 1, pos + 1, logits[:B], nxt[:B])
-        for w in range(3):
-            step(ctx + w)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(steps):
-            step(ctx + 3 + i)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / steps
-        res = {"ms_per_step": round(ms, 4), "tok_s": round(B * 1e3 / ms, 1)}
-        # The same steps captured as one HIP graph and replayed (positions
-        # of every step in device memory at fixed addresses; the attention
-        # planned for the last step's length); the graph's last logits must
-        # equal an eager step's bit for bit.
-        base = ctx + 3 + steps
-        pos_all = torch.tensor([[base + i] * B for i in range(steps)], dtype=torch.int32,
-                               device="cuda")
-        seq_all = pos_all + 1
-        cap_len = base + steps
-
-        def gstep(i, lg):
-            model.decode_paged(toks, pool, P, bt[:B], per, pos_all[i], seq_all[i], cap_len, lg,
+        def step(i, lg):
+            model.decode_paged(toks, pool, P, bt[:B], per, pos_b[i], seq_b[i], cap_len, lg,
                                nxt[:B])
+
+        def eager():
+            for i in range(steps):
+                step(i, logits[:B])
+        for i in range(3):
+            step(i, logits[:B])
+        torch.cuda.synchronize()
+        res = {}
+        g = None
         try:
-            for i in range(2):
-                gstep(i, logits[:B])
-            torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             cs = torch.cuda.Stream()
             cs.wait_stream(torch.cuda.current_stream())
             with torch.cuda.graph(g, stream=cs, capture_error_mode="thread_local"):
-                for i in range(steps):
-                    gstep(i, logits[:B])
+                eager()
             torch.cuda.current_stream().wait_stream(cs)
             g.replay()
             torch.cuda.synchronize()
             ref = torch.empty_like(logits[:B])
-            gstep(steps - 1, ref)
+            step(steps - 1, ref)
             torch.cuda.synchronize()
-            same = torch.equal(ref, logits[:B])
-            if same:
+            if not torch.equal(ref, logits[:B]):
+                res["graph_error"] = "graph logits differ from an eager step"
+                g = None
+        except Exception as exc:  # capture unsupported here: eager figures only
+            res["graph_error"] = str(exc)[:200]
+            g = None
+        te, tg = [], []
+        for _ in range(rounds):
+            for fn, acc in ((eager, te), (g.replay if g is not None else None, tg)):
+                if fn is None:
+                    continue
+                e0, e1 = ev(), ev()
                 e0.record()
-                g.replay()
+                fn()
                 e1.record()
                 torch.cuda.synchronize()
-                gms = e0.elapsed_time(e1) / steps
-                res["graph"] = {"ms_per_step": round(gms, 4), "tok_s": round(B * 1e3 / gms, 1)}
-            else:
-                res["graph"] = {"error": "graph logits differ from an eager step"}
-            del g
-        except Exception as exc:  # capture unsupported here: eager figure only
-            res["graph"] = {"error": str(exc)[:200]}
+                acc.append(e0.elapsed_time(e1) / steps)
+        ms = float(np.median(te))
+        res.update({"ms_per_step": round(ms, 4), "tok_s": round(B * 1e3 / ms, 1),
+                    "ms_min": round(min(te), 4), "ms_max": round(max(te), 4)})
+        if tg:
+            gms = float(np.median(tg))
+            res["graph"] = {"ms_per_step": round(gms, 4), "tok_s": round(B * 1e3 / gms, 1),
+                            "ms_min": round(min(tg), 4), "ms_max": round(max(tg), 4)}
+        del g
         out[f"B{B}"] = res
     model.close()
-    return {"workload": f"config-5 model, batched runner, ctx {ctx}; eager launches, and the "
-                        "same steps replayed from one HIP graph (graph)", **out}
+    return {"workload": f"config-5 model, batched runner, ctx {ctx}; {steps} steps launched "
+                        "eagerly and the same steps replayed from one HIP graph (graph), timed "
+                        f"alternately {rounds} times (median, min, max per step)", **out}
 
 
 def traffic_from_profile(dbytes):
@@ -1045,7 +1111,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(dbytes),
-                     "kernel": "decode_splitk_kernel<128,4,true> (append fused) + "
+                     "kernel": "decode_splitk_kernel<128,4,true,1> (append fused) + "
                                "decode_merge_kernel<128,4>: one kvhp_paged_append_decode call",
                      "avg_launch_us": round(r["step_us_region"], 2),
                      "per_step_event_us": {"median": round(r["step_us_median"], 2),
@@ -1084,11 +1150,15 @@ def main():
     del c
     torch.cuda.empty_cache()
     extra = {}
-    parts = set(args.only.split(",")) if args.only else {"c1", "c2", "c4", "c5", "c5b", "kv"}
+    parts = set(args.only.split(",")) if args.only else {"c1", "c2", "c4", "c5", "c5b", "kv",
+                                                           "layout"}
     if not args.no_extra:
         if "kv" in parts:
             log("kv movement ...")
             extra["kv_movement"] = run_kv_movement(torch, kvhp)
+        if "layout" in parts:
+            log("page layout ...")
+            extra["page_layout"] = run_page_layout(torch, kvhp)
         if "c1" in parts:
             log("config1 ...")
             extra["config1"] = run_config1(torch, kvhp)

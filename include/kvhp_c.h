@@ -88,7 +88,8 @@ int kvhp_stream_read(const void* buf, size_t bytes, void* sink, void* stream);
  * reference probe, src/cuda/read_bandwidth.cu:8-118, for the access pattern
  * of a paged decode): reads the pages page_ids[0..n_ids) of `pool`
  * (pool_bytes of device memory cut into pages of page_bytes = 2048 or 4096,
- * the page of one KV head at D = 64 or 128) once each with 16-byte
+ * the page of one KV head at D = 64 or 128, or 8192 / 16384 / 32768 to
+ * measure coarser layouts) once each with 16-byte
  * non-temporal loads; ids outside the pool are clamped into it.  Writes
  * nothing but possibly the 4-byte sink, as above.  With a random page order
  * and as many pages as a decode step reads, its rate is the ceiling of that

@@ -13,10 +13,10 @@
 // (temporal) loads ~1 TB/s less than non-temporal ones; the contiguous form
 // is the device's streaming-read ceiling.
 //
-// page_read_kernel reads a list of pages (2 or 4 KB, the page of one KV head
-// at D = 64 or 128) in list order, one wave per workgroup, four pages in
-// flight per wave: the ceiling of a paged decode that reads the same pages
-// in a random order.
+// page_read_kernel reads a list of pages (2 or 4 KB: the page of one KV head
+// at D = 64 or 128; up to 32 KB to measure coarser layouts) in list order,
+// one wave per workgroup, 16 KB of pages in flight per wave: the ceiling of
+// a paged decode that reads the same pages in a random order.
 #include "kvhp_internal.h"
 
 #include <algorithm>
@@ -50,14 +50,14 @@ stream_read_kernel(const u32x4* p, size_t n16, uint32_t* sink) {
     if (acc == kSinkMagic) *sink = acc;
 }
 
-constexpr int kPagesInFlight = 4;
-
-// LPP: 1 KB wave loads per page (2: 2 KB pages, 4: 4 KB pages).  Wave w reads
-// list entries [w*per, (w+1)*per); ids outside the pool are clamped into it.
+// LPP: 1 KB wave loads per page (2 to 32: pages of 2 to 32 KB), PIF pages in
+// flight per wave (16 KB in flight, at least one page).  Wave w reads list
+// entries [w*per, (w+1)*per); ids outside the pool are clamped into it.
 template <int LPP>
 __global__ void __launch_bounds__(kWave)
 page_read_kernel(const u32x4* pool, int64_t pool_pages, const int32_t* ids, int64_t n_ids,
                  int64_t per, uint32_t* sink) {
+    constexpr int kPagesInFlight = LPP >= 16 ? 1 : 16 / LPP;
     const int lane = threadIdx.x;
     const int64_t beg = (int64_t)blockIdx.x * per;
     const int64_t end = beg + per < n_ids ? beg + per : n_ids;
@@ -111,27 +111,36 @@ extern "C" int kvhp_page_read(const void* pool, int64_t pool_bytes, const int32_
     if (n_ids <= 0) return KVHP_OK;
     KVHP_REQUIRE(pool && page_ids && sink, KVHP_ERR_INVALID, "page_read: null pointer");
     KVHP_REQUIRE(aligned16(pool), KVHP_ERR_INVALID, "page_read: pool not 16-byte aligned");
-    KVHP_REQUIRE(page_bytes == 2048 || page_bytes == 4096, KVHP_ERR_UNSUPPORTED,
-                 "page_read: page_bytes %d is neither 2048 nor 4096", page_bytes);
+    KVHP_REQUIRE(page_bytes == 2048 || page_bytes == 4096 || page_bytes == 8192 ||
+                     page_bytes == 16384 || page_bytes == 32768,
+                 KVHP_ERR_UNSUPPORTED, "page_read: page_bytes %d is not a power of two in 2..32 KB",
+                 page_bytes);
     const int64_t pool_pages = pool_bytes / page_bytes;
     KVHP_REQUIRE(pool_pages > 0, KVHP_ERR_INVALID, "page_read: pool smaller than a page");
     int dev = 0, cus = 0;
     KVHP_HIP(hipGetDevice(&dev), "hipGetDevice");
     KVHP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
              "hipDeviceGetAttribute");
-    // eight waves per CU, each a contiguous share of the list
+    // eight waves per CU, each a contiguous share of the list (16 KB of
+    // pages per wave at a time)
+    const int pif = page_bytes >= 16384 ? 1 : 16384 / page_bytes;
     const int64_t want = (int64_t)(cus > 0 ? cus : 256) * 8;
-    const int64_t waves = std::min<int64_t>(want, (n_ids + kPagesInFlight - 1) / kPagesInFlight);
+    const int64_t waves = std::min<int64_t>(want, (n_ids + pif - 1) / pif);
     const int64_t per = (n_ids + waves - 1) / waves;
     const int64_t grid = (n_ids + per - 1) / per;
     auto* p = static_cast<const u32x4*>(pool);
     auto* sk = static_cast<uint32_t*>(sink);
     auto s = static_cast<hipStream_t>(stream);
-    if (page_bytes == 4096)
-        hipLaunchKernelGGL(page_read_kernel<4>, dim3(static_cast<unsigned>(grid)), dim3(kWave), 0, s,
-                           p, pool_pages, page_ids, n_ids, per, sk);
-    else
-        hipLaunchKernelGGL(page_read_kernel<2>, dim3(static_cast<unsigned>(grid)), dim3(kWave), 0, s,
-                           p, pool_pages, page_ids, n_ids, per, sk);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kWave), 0, s, p,
+                           pool_pages, page_ids, n_ids, per, sk);
+    };
+    switch (page_bytes) {
+        case 2048: go(page_read_kernel<2>); break;
+        case 4096: go(page_read_kernel<4>); break;
+        case 8192: go(page_read_kernel<8>); break;
+        case 16384: go(page_read_kernel<16>); break;
+        default: go(page_read_kernel<32>); break;
+    }
     return check_launch("page_read");
 }

@@ -27,7 +27,7 @@ def test_probe_argument_checks():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("page_bytes", [2048, 4096])
+@pytest.mark.parametrize("page_bytes", [2048, 4096, 8192, 16384, 32768])
 def test_probes_run(page_bytes):
     import torch
     buf = torch.ones((8 << 20) // 4, dtype=torch.float32, device="cuda")
