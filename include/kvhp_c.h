@@ -176,9 +176,10 @@ int kvhp_decode_attention(const void* q, const kvhp_kv_view* k_view,
  * or threads) race.  Partials need no clearing: a call reads only the ones
  * it wrote.  The first call on a device resolves the array's address and
  * its kernels' occupancy (no allocation, no stream work): make that first
- * call, with the shapes to be captured, outside graph capture; later calls
- * may be captured (tested: two calls in one graph, replays bit-identical to
- * eager kvhp_decode_attention). */
+ * call, with the shapes to be captured, outside graph capture (a first call
+ * under capture is refused with KVHP_ERR_INVALID, nothing enqueued); later
+ * calls may be captured (tested: two calls in one graph, replays
+ * bit-identical to eager kvhp_decode_attention). */
 int kvhp_decode_attention_noalloc(const void* q, const kvhp_kv_view* k_view,
                                   const kvhp_kv_view* v_view, const int32_t* seq_lens,
                                   void* out, int batch, int num_q_heads, int num_kv_heads,

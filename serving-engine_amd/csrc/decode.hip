@@ -953,12 +953,19 @@ static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 std::mutex g_scratch_mutex;
 std::vector<void*> g_scratch;   // device address of `scratch`, per device
 
-int scratch_address(void** out) {
+int scratch_address(void** out, hipStream_t s) {
     int dev = 0;
     KVHP_HIP(hipGetDevice(&dev), "hipGetDevice");
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if ((int)g_scratch.size() <= dev) g_scratch.resize(dev + 1, nullptr);
     if (!g_scratch[dev]) {
+        // The address is resolved once per device, outside any graph capture
+        // (the symbol lookup is not a stream operation a graph can record).
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        KVHP_HIP(hipStreamIsCapturing(s, &st), "hipStreamIsCapturing(noalloc)");
+        KVHP_REQUIRE(st == hipStreamCaptureStatusNone, KVHP_ERR_INVALID,
+                     "decode_attention_noalloc: the first call on device %d is under graph "
+                     "capture; make one call outside capture first", dev);
         void* p = nullptr;
         KVHP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
         g_scratch[dev] = p;
@@ -1313,7 +1320,7 @@ extern "C" int kvhp_decode_attention_noalloc(const void* q, const kvhp_kv_view* 
                  "scratch holds %zu (use kvhp_decode_attention with a workspace)",
                  need, kScratchBytes);
     void* ws = nullptr;
-    const int rc = scratch_address(&ws);
+    const int rc = scratch_address(&ws, static_cast<hipStream_t>(stream));
     if (rc) return rc;
     return decode_attention_impl(q, k_view, v_view, seq_lens, 0, out, batch, num_q_heads,
                                  num_kv_heads, head_dim, max_seq_len, num_splits, ws,

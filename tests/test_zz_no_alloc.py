@@ -156,3 +156,55 @@ def test_noalloc_captured_in_a_graph_replays_bit_exact():
             assert np.array_equal(from_gpu(o).view(np.uint16), from_gpu(want).view(np.uint16)), \
                 f"replay {r}, call {i}: graph output differs from the eager call"
     del g
+
+
+_FIRST_CALL_SCRIPT = r"""
+import sys
+sys.path[:0] = sys.argv[1:]
+import torch, kvhp
+hq, hkv, d, L = 32, 8, 128, 300
+k = torch.randn((1, hkv, L, d), device="cuda").half()
+view = kvhp.strided_view(k, hkv * L * d, L * d, d)
+q = torch.randn((1, hq, d), device="cuda").half()
+lens = torch.tensor([L], dtype=torch.int32, device="cuda")
+out = torch.zeros((1, hq, d), dtype=torch.float16, device="cuda")
+torch.cuda.synchronize()
+cs = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+err = None
+with torch.cuda.stream(cs):
+    g.capture_begin()
+    try:
+        kvhp.decode_attention_noalloc(q, view, view, lens, out, hq, hkv, d, L, 4)
+    except kvhp.KVHPError as e:
+        err = e
+    finally:
+        g.capture_end()
+torch.cuda.synchronize()
+del g
+assert err is not None and err.code == kvhp.KVHP_ERR_INVALID and "first call" in str(err), err
+kvhp.decode_attention_noalloc(q, view, view, lens, out, hq, hkv, d, L, 4)   # outside capture
+want = torch.zeros_like(out)
+kvhp.decode_attention(q, view, view, lens, want, hq, hkv, d, L, 4)
+torch.cuda.synchronize()
+assert torch.equal(out, want)
+print("first-call rule ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_is_refused():
+    """In a fresh process (the scratch address not yet resolved): a first
+    noalloc call under graph capture is refused with KVHP_ERR_INVALID before
+    anything is enqueued; the next call outside capture works and matches
+    kvhp_decode_attention bit for bit."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    paths = [os.path.join(root, "serving-engine_amd"), os.path.join(root, "oracle"), here]
+    note("noalloc first call under capture (subprocess)")
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_SCRIPT] + paths, capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "first-call rule ok" in r.stdout
