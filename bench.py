@@ -797,7 +797,7 @@ def run_config2(torch, kvhp, stream_gbps=None, splits=(1, 4, 16, 64, 0), reps=15
     return {"workload": "config2: B=1, 32/8 heads, D=128, contiguous fp16 KV, flushed", "rows": rows}
 
 
-def run_config4(torch, kvhp, sizes=(512, 2048, 8192), reps=10, attention_only=True):
+def run_config4(torch, kvhp, sizes=(512, 2048, 4096, 8192), reps=10, attention_only=True):
     """causal prefill that writes K/V into 16-token pages as
     it runs (kvhp_flash_prefill_paged, a seeded random page permutation); the
     same prefill without the page writes is reported beside it."""

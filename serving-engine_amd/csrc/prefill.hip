@@ -3,12 +3,13 @@
 // Work decomposition: a 512-thread workgroup (8 waves) owns one KV head and
 // a query block of 32*RB rows for all G query heads of that KV head: G*RB
 // units of (head, 32 rows).  With KG = 1 each wave owns one unit (RB = 8/G);
-// for short prompts (KG = 2, G <= 4) two wave groups share the units and
-// split every tile's keys, doubling the workgroup count.  Each 64-key K/V
+// with KG = 2 (G <= 4; chosen where doubling the workgroup count fills the
+// CUs without adding a round, e.g. S <= 2048 at B = 1) two wave groups share
+// the units and split every tile's keys.  Each 64-key K/V
 // tile is read from HBM once per workgroup and consumed by all 8 waves, so
 // GQA heads share their K/V traffic.  Query blocks i and N-1-i are processed
 // by the same workgroup (two passes), giving every workgroup the same causal
-// work (short prompts: odd KV heads run the long block first), when those
+// work (KG = 2: odd KV heads run the long block first), when those
 // pairs fill the GPU; below that (S < 2048 at 32/8 heads) every block gets
 // its own workgroup, longest first, so that more CUs share the work (S=512
 // 15.4 vs 21.5 us).  Grid x enumerates (pair or block, kv_head) with the kv
@@ -141,7 +142,7 @@ __device__ __forceinline__ float halves_sum(float x) {
 // form two groups of four that share the units and split every 64-key tile
 // (group y takes keys 32y..32y+31), and the two softmax states of a unit are
 // merged through LDS at the end -- half the query rows per workgroup, so
-// twice the workgroups for short prompts.  K/V tiles of 64 keys stream through a 4-stage LDS ring
+// twice the workgroups.  K/V tiles of 64 keys stream through a 4-stage LDS ring
 // filled by direct global->LDS loads and are read by every wave, so GQA
 // heads share their K/V traffic; rows are stored XOR-swizzled (16-byte
 // chunk c of row r at position c ^ swz(r)) so the operand reads hit distinct
@@ -260,7 +261,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
 
     for (int pass = 0; pass < 2; ++pass) {
-        // Short prompts: odd KV heads (other XCDs) take their long block
+        // KG = 2: odd KV heads (other XCDs) take their long block
         // first, so that half the workgroups load Q and drain stores while
         // the other half run tile loops (every workgroup of a KV head still
         // walks the same tiles together).
@@ -674,13 +675,19 @@ int prefill_impl(const void* q, const void* k, const void* v, void* out, int64_t
                       (!pool_k || (aligned16(pool_k) && aligned16(pool_v)));
     if (fast) {
         // units of (head, 32 rows) per workgroup: one per wave, or (G <= 4)
-        // one per pair of waves that split each tile's keys
-        // Split each tile's keys across two wave groups (twice the
-        // workgroups) only when one unit per wave would leave fewer than two
-        // workgroups per CU: the split halves the work per barrier.
+        // one per pair of waves that split each tile's keys (KG = 2: twice
+        // the workgroups, each with half the rows).  A KG = 2 workgroup takes
+        // ~57 % of a KG = 1 workgroup's time, so KG = 2 pays when doubling
+        // the workgroups adds no round of CUs: with grid1 block pairs of one
+        // unit per wave, up to half the CUs (grid1 <= 128) or one and a half
+        // rounds (257..384).  Measured at 32/8 heads, D = 128: KG = 1 is
+        // 12-32 % faster at grid1 = 144..256 (S = 2304..4096 at B = 1,
+        // S = 1280..2048 at B = 2), 10 % at 448 and 8 % at 512; KG = 2 is
+        // 19 % faster at 128 (S = 2048) and 1-10 % at 288..384.
         const int64_t qblk1 = (seq_len + 32 * (8 / a.G) - 1) / (32 * (8 / a.G));
         const int64_t grid1 = (int64_t)hkv * ((qblk1 + 1) / 2) * batch;
-        const int kg = ((a.G == 1 || a.G == 2 || a.G == 4) && grid1 < 2 * kNumCUs) ? 2 : 1;
+        const bool split = grid1 <= kNumCUs / 2 || (grid1 > kNumCUs && grid1 <= kNumCUs * 3 / 2);
+        const int kg = ((a.G == 1 || a.G == 2 || a.G == 4) && split) ? 2 : 1;
         a.RB = 8 / kg / a.G;
         const int bm = 32 * a.RB;
         a.n_qblk = static_cast<int>((seq_len + bm - 1) / bm);

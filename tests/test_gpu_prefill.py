@@ -131,8 +131,9 @@ def test_prefill_pair_pass_full_check(s, hq, hkv, d, batch):
         assert_attn_close(got[i], ref, f"batch {i}")
 
 
-@pytest.mark.parametrize("s,hq,hkv,d", [(8192, 32, 8, 128), (2048, 32, 8, 128), (333, 14, 2, 64),
-                                        (70, 6, 3, 96), (515, 8, 4, 128), (200, 4, 4, 64)])
+@pytest.mark.parametrize("s,hq,hkv,d", [(8192, 32, 8, 128), (2048, 32, 8, 128), (2560, 32, 8, 128),
+                                        (333, 14, 2, 64), (70, 6, 3, 96), (515, 8, 4, 128),
+                                        (200, 4, 4, 64)])
 def test_prefill_paged_writes_pages_bit_exact(s, hq, hkv, d):
     """flash_prefill_paged writes K/V rows into the pages exactly as the paged
     append does (config 4: K/V written into 16-token pages as produced), and
@@ -197,3 +198,21 @@ def test_causal_gqa_api_routes_to_prefill():
     ref = oracle.causal_gqa(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32),
                             hq, hkv, d)
     assert_attn_close(from_gpu(out).astype(np.float32), ref, "causal_gqa")
+
+
+@pytest.mark.parametrize("s,hq,hkv,d,batch", [
+    (2560, 32, 8, 128, 1), (4096, 32, 8, 128, 1), (2048, 32, 8, 128, 2), (6144, 32, 8, 128, 1),
+    (5000, 16, 4, 64, 1),
+])
+def test_prefill_key_group_choice_shapes(s, hq, hkv, d, batch):
+    """Prompt sizes on either side of the key-group choice (one unit per wave
+    for 129..256 and 385+ block pairs, two key groups for up to 128 and
+    257..384; paired or one block per workgroup): both rows at every 32-row
+    block edge and a seeded sample, every head, against the oracle."""
+    rng = np.random.default_rng(11 * s + d + batch)
+    q = oracle.normal_f16(rng, (batch, s, hq, d))
+    k, v = oracle.normal_f16(rng, (batch, s, hkv, d)), oracle.normal_f16(rng, (batch, s, hkv, d))
+    note(f"prefill key-group choice S={s} Hq={hq} Hkv={hkv} D={d} B={batch}")
+    got = _prefill(q, k, v, hq, hkv, d, batch=batch)
+    for i in range(batch):
+        _check_rows(got[i], q[i], k[i], v[i], hq, hkv, d, _edge_rows(rng, s, 8), f"S={s} batch {i}")
