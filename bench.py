@@ -763,11 +763,12 @@ def run_config1(torch, kvhp):
     return res
 
 
-def run_config2(torch, kvhp, stream_gbps=None, splits=(1, 4, 16, 64, 0), reps=15):
+def run_config2(torch, kvhp, stream_gbps=None, splits=(1, 4, 16, 64, 0), reps=15,
+                contexts=(4096, 16384, 65536)):
     hq, hkv, d = 32, 8, 128
     fl = Flusher(torch)
     rows = []
-    for L in (4096, 16384, 65536):
+    for L in contexts:
         g = torch.Generator(device="cuda").manual_seed(L)
         kc = torch.randn((1, hkv, L, d), generator=g, device="cuda").half()
         vc = torch.randn((1, hkv, L, d), generator=g, device="cuda").half()
