@@ -367,6 +367,17 @@ int launch_gemv(const GemvArgs& a, hipStream_t s) {
     return check_launch("gemv");
 }
 
+// Workgroup barrier that orders LDS only: this wave's LDS reads and writes
+// complete (lgkmcnt(0)) before s_barrier, and its global loads stay in
+// flight.  __syncthreads() would also wait for every outstanding global load:
+// the weights the MFMAs need next and the next tile's prefetch.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt and expcnt left free
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ---- Batched decode projections (B <= 32 sequences per step) -----------------
 // Y[b][n] = sum_k W[n][k] X[b][k] on v_mfma_f32_16x16x32_f16 with the weights
 // as the A operand.  A tile is 16 weight rows; for the paired epilogues its
@@ -421,8 +432,23 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
     // Two weight buffers where the registers allow (8-wave workgroups);
     // otherwise each tile loads its weights at its start.
     constexpr bool kDB = !kSeq && (NWMAX <= 8 || (2 + NBT) * C * 4 <= 100);
-    __shared__ float red[2][NWMAX][NBT][256];
+    // 256-wide slices (K <= 2048): each wave stages its x slice through its
+    // own LDS region with contiguous loads (512 bytes of a row per 32 lanes),
+    // then reads it back in the MFMA layout.  Loaded directly in that layout
+    // (16 rows of 64 bytes, 4 KB apart, per instruction) the same bytes took
+    // 4.7 us per launch at B = 32 against 3.4 us staged (2.5 us read
+    // linearly, 1.6 us for an empty launch).
+    constexpr bool kStage = !kSeq && C == 8;
+    constexpr int kCH = 4 * C;                           // 16-byte chunks per slice row
+    constexpr int kRedBytes = 2 * NBT * 256 * 4;         // a wave's two partial-sum buffers
+    constexpr int kStgBytes = kStage ? NBT * 16 * kCH * 16 : 0;
+    constexpr int kWaveBytes = kRedBytes > kStgBytes ? kRedBytes : kStgBytes;
+    // per wave: the x stage, then (once x is in registers) the partial sums
+    __shared__ __attribute__((aligned(16))) char lds[NWMAX * kWaveBytes];
     __shared__ float ssq[NBT][NWMAX][16];
+    auto red = [&](int rb, int wi, int bt) {
+        return reinterpret_cast<float*>(lds + wi * kWaveBytes) + (rb * NBT + bt) * 256;
+    };
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int NW = static_cast<int>(blockDim.x >> 6);
     const int g = lane >> 4, col = lane & 15;
@@ -479,8 +505,21 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
     // x slice of every batch tile, resident for all tiles (RMSNorm applied)
     half8 xr[kSeq ? 1 : NBT][C];
     if constexpr (!kSeq) {
+        // staged: lane i of load j takes chunk (64j + i) % kCH of slice row
+        // (64j + i) / kCH; rows past B load nothing (zero)
+        constexpr int kNL = kStage ? NBT * 16 * kCH / kWave : 1;
+        half8 stg[kNL];
+        if constexpr (kStage) {
+            const f16* xs0 = a.x + sl * 32 * C;
 #pragma unroll
-        for (int bt = 0; bt < NBT; ++bt) load_x(bt, xr[bt]);
+            for (int j = 0; j < kNL; ++j) {
+                const int idx = j * kWave + lane, row = idx / kCH, ch = idx % kCH;
+                stg[j] = row < a.B ? load_half8(xs0 + (int64_t)row * a.K + 8 * ch) : half8{};
+            }
+        } else {
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) load_x(bt, xr[bt]);
+        }
         half8 nw[C];
         if constexpr (RMS) {
 #pragma unroll
@@ -492,6 +531,22 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
         // every load above in flight before the first use (one round trip;
         // the scheduler would otherwise pair loads with their uses)
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kStage) {
+            // into this wave's region (chunk c of row r at c ^ (r & 7): the
+            // 8-lane phases of both the writes and the operand reads hit
+            // distinct banks), then back in the layout of the B operand
+            half8* st = reinterpret_cast<half8*>(lds + w * kWaveBytes);
+#pragma unroll
+            for (int j = 0; j < kNL; ++j) {
+                const int idx = j * kWave + lane, row = idx / kCH, ch = idx % kCH;
+                st[row * kCH + (ch ^ (row & 7))] = stg[j];
+            }
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+                for (int t = 0; t < C; ++t)
+                    xr[bt][t] = st[(16 * bt + col) * kCH + ((g + 4 * t) ^ (col & 7))];
+        }
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt)
             if (16 * bt + col >= a.B)
@@ -511,7 +566,7 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
                 ss = rows4_sum(ss);
                 if (g == 0) ssq[bt][w][col] = ss;
             }
-            __syncthreads();
+            lds_barrier();   // the weights keep landing under the scaling below
 #pragma unroll
             for (int bt = 0; bt < NBT; ++bt) {
                 float tot = 0.f;
@@ -549,8 +604,9 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
         float v0 = 0.f, v1 = 0.f;
         for (int i = 0; i < NW; ++i) {   // slice i sits in wave (i - rot) mod NW
             const int wi = i >= rot ? i - rot : i - rot + NW;
-            v0 += red[rb][wi][bt][m * 16 + n];
-            if constexpr (kPair) v1 += red[rb][wi][bt][(m + P) * 16 + n];
+            const float* rp = red(rb, wi, bt);
+            v0 += rp[m * 16 + n];
+            if constexpr (kPair) v1 += rp[(m + P) * 16 + n];
         }
         if constexpr (EPI == kEpiQKV) {
             const int tph = a.D / L;
@@ -630,10 +686,14 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
             }
         }
 #pragma unroll
-        for (int bt = 0; bt < NBT; ++bt)
+        for (int bt = 0; bt < NBT; ++bt) {
+            float* rp = red(rb, w, bt);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) red[rb][w][bt][(4 * g + e) * 16 + col] = acc[bt][e];
-        __syncthreads();
+            for (int e = 0; e < 4; ++e) rp[(4 * g + e) * 16 + col] = acc[bt][e];
+        }
+        // LDS-only: the next tile's weights (prefetched above) stay in flight
+        // through the barrier and the epilogue
+        lds_barrier();
         for (int o = o0; o < NBT * kOut; o += static_cast<int>(blockDim.x)) {
             if (o == o0) {
                 epilogue(tl, o, rb, static_cast<float>(r0), pos0, pid0);
