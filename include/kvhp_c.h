@@ -316,6 +316,44 @@ int kvhp_rmsnorm_qkv_rope_append_rows(const void* W_qkv, const void* x, const vo
                                       const int32_t* block_tables, int max_pages, int num_pages,
                                       int num_q_heads, int num_kv_heads, int head_dim, int K,
                                       int batch, void* stream);
+/* No counterpart in the reference (its batched projections are library
+ * GEMMs).  The batched projections above over weights pre-tiled for them:
+ * kvhp_rows_tile_weights copies W (row-major, as the calls above take it)
+ * into kvhp_rows_tiled_bytes bytes in which every 16-row tile keeps, per
+ * 32-wide k step, the 64 MFMA lanes' 16-byte operands contiguous (rows in
+ * the order the kernels pair them: SwiGLU gate/up rows, RoPE dimension
+ * pairs), so one wave's weight load is 1 KB contiguous instead of 16 rows of
+ * 64 bytes.  kind: KVHP_ROWS_PLAIN (the residual / fp16 / fp32 calls,
+ * N rows), KVHP_ROWS_SWIGLU (W_gate_up, N gate rows then N up rows),
+ * KVHP_ROWS_QKV (N ignored: (Hq + 2 Hkv) head_dim rows).  The *_tiled calls
+ * take the tiled copy in place of W, with the arguments of their row-major
+ * counterparts (kvhp_gemv_residual_rows_tiled that of _ws: workspace NULL or
+ * 0 bytes for the single-launch path), and give bit-identical outputs.
+ * Unsupported shapes (those the row-major calls refuse): size 0,
+ * KVHP_ERR_UNSUPPORTED. */
+#define KVHP_ROWS_PLAIN 0
+#define KVHP_ROWS_SWIGLU 1
+#define KVHP_ROWS_QKV 2
+size_t kvhp_rows_tiled_bytes(int kind, int N, int K, int num_q_heads, int num_kv_heads,
+                             int head_dim);
+int kvhp_rows_tile_weights(int kind, const void* W, int N, int K, int num_q_heads,
+                           int num_kv_heads, int head_dim, void* W_tiled, void* stream);
+int kvhp_gemv_residual_rows_tiled(const void* W_tiled, const void* x, const void* r, void* y,
+                                  int N, int K, int batch, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+int kvhp_rmsnorm_gemv_rows_tiled(const void* W_tiled, const void* x, const void* norm_w,
+                                 float eps, void* y16, float* y32, int N, int K, int batch,
+                                 void* stream);
+int kvhp_rmsnorm_gemv_swiglu_rows_tiled(const void* W_tiled, const void* x, const void* norm_w,
+                                        float eps, void* out, int N, int K, int batch,
+                                        void* stream);
+int kvhp_rmsnorm_qkv_rope_append_rows_tiled(const void* W_tiled, const void* x,
+                                            const void* norm_w, float eps,
+                                            const int32_t* positions, float rope_theta,
+                                            void* q_out, void* pool_k, void* pool_v,
+                                            const int32_t* block_tables, int max_pages,
+                                            int num_pages, int num_q_heads, int num_kv_heads,
+                                            int head_dim, int K, int batch, void* stream);
 /* Replaces engine::cuda::rmsnorm (kernels.h:24-32): rows x dim, fp32 math. */
 int kvhp_rmsnorm(const void* x, const void* weight, void* out, int64_t rows, int64_t dim,
                  float eps, void* stream);
@@ -454,8 +492,12 @@ int kvhp_llama_prefill_cached(void* model, const int32_t* tokens, int n, int num
  * keys (<= max_seq_len; the caller has already bumped it, so positions[b] =
  * seq_lens[b] - 1), and ends in fp32 logits [batch][V] and greedy
  * next_tokens[batch] (lowest index on ties).  Up to 32 sequences run on the
- * fused batched projections (kvhp_*_rows: each weight read once per step);
- * larger batches on library GEMMs.  Asynchronous on `stream`. */
+ * fused batched projections (kvhp_*_rows_tiled: each weight read once per
+ * step, from the model's tiled copy of it, which the first such step builds
+ * on `stream` -- as large as the four projections and the LM head; weights
+ * written through kvhp_llama_tensor after that are seen by batched steps once
+ * kvhp_llama_reserve rebuilds the copies); larger batches on library GEMMs.
+ * Asynchronous on `stream`. */
 int kvhp_llama_decode_paged(void* model, const int32_t* tokens, int batch, void* pool,
                             int num_pages, const int32_t* block_tables, int max_pages,
                             const int32_t* positions, const int32_t* seq_lens, int max_seq_len,
@@ -463,7 +505,9 @@ int kvhp_llama_decode_paged(void* model, const int32_t* tokens, int batch, void*
 /* Sizes the model's own decode buffers (split-attention partials, the
  * batched down projection's K-split partials) for every kvhp_llama_decode_paged
  * call with batch <= max_batch and max_seq_len <= max_seq_len, so that such
- * calls allocate nothing.  No reference counterpart (the reference sizes its
+ * calls allocate nothing, and (max_batch > 1) builds or rebuilds the batched
+ * projections' tiled weights from the current weights, synchronously.  No
+ * reference counterpart (the reference sizes its
  * split buffer once at load, forward_gpu.cu:100).  A call that needs larger
  * buffers grows them (the old ones stay allocated until kvhp_llama_destroy,
  * so graphs captured earlier keep valid addresses); under HIP graph capture it

@@ -53,6 +53,9 @@ struct Layer {
     f16* w_o = nullptr;        // [H][Hq D]
     f16* w_gate_up = nullptr;  // [2F][H]
     f16* w_down = nullptr;     // [H][F]
+    // the four projections tiled for the batched kernels (kvhp_rows_tile_weights);
+    // built on the first batched step, rebuilt by kvhp_llama_reserve
+    f16 *w_qkv_t = nullptr, *w_o_t = nullptr, *w_gate_up_t = nullptr, *w_down_t = nullptr;
     f16* pool_k = nullptr;     // [Hkv][P][16][D]
     f16* pool_v = nullptr;
 };
@@ -92,6 +95,8 @@ struct Model {
     size_t part_rows_bytes = 0;
     int prompt_len = 0;
     bool rows_ok = false;      // batched projections fit the skinny-GEMM kernels
+    f16* lm_head_t = nullptr;  // LM head tiled for the batched kernels
+    bool tiled = false;        // the tiled copies hold the current weights
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
 
@@ -363,6 +368,40 @@ int prefill_suffix_layers(Model& m, int first, int n, const Pages& pg, const int
 // runs on the batch-1 step's GEMV kernels, up to 32 on the fused skinny-GEMM
 // kernels, larger batches on library GEMMs with separate RMSNorm / RoPE /
 // SwiGLU launches.
+// Tiled copies of the projection weights for the batched kernels (each weight
+// load 1 KB contiguous; bit-identical outputs): allocated once, (re)written
+// from the row-major weights on stream s.  Not under graph capture (an
+// allocation and copies a replay must not repeat): kvhp_llama_reserve builds
+// them before.
+int build_tiled(Model& m, hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    KVHP_HIP(hipStreamIsCapturing(s, &st), "hipStreamIsCapturing(tiled weights)");
+    KVHP_REQUIRE(st == hipStreamCaptureStatusNone, KVHP_ERR_WORKSPACE,
+                 "decode_paged: the batched projections' tiled weights are built on the first "
+                 "batched step, which cannot happen under graph capture (call "
+                 "kvhp_llama_reserve before capturing)");
+    const kvhp_llama_config& c = m.c;
+    const int H = c.hidden_size, D = c.head_dim, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
+    const int F = c.ffn_size;
+    auto tile = [&](f16** dst, int kind, const f16* W, int N, int K) {
+        if (!*dst) {
+            const size_t nb = kvhp_rows_tiled_bytes(kind, N, K, Hq, Hkv, D);
+            KVHP_REQUIRE(nb > 0, KVHP_ERR_UNSUPPORTED, "tiled weights: %d x %d", N, K);
+            KVHP_TRY(alloc_n(m, nb / sizeof(f16), dst));
+        }
+        return kvhp_rows_tile_weights(kind, W, N, K, Hq, Hkv, D, *dst, s);
+    };
+    for (Layer& L : m.layers) {
+        KVHP_TRY(tile(&L.w_qkv_t, KVHP_ROWS_QKV, L.w_qkv, 0, H));
+        KVHP_TRY(tile(&L.w_o_t, KVHP_ROWS_PLAIN, L.w_o, H, Hq * D));
+        KVHP_TRY(tile(&L.w_gate_up_t, KVHP_ROWS_SWIGLU, L.w_gate_up, F, H));
+        KVHP_TRY(tile(&L.w_down_t, KVHP_ROWS_PLAIN, L.w_down, H, F));
+    }
+    KVHP_TRY(tile(&m.lm_head_t, KVHP_ROWS_PLAIN, m.lm_head, c.vocab_size, H));
+    m.tiled = true;
+    return KVHP_OK;
+}
+
 int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                 const int32_t* positions, const int32_t* seq_lens, int max_seq_len,
                 float* logits, int32_t* next, void* s, const int32_t* write_bt = nullptr) {
@@ -378,6 +417,8 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
     void* ws = nullptr;
     size_t ws_bytes = 0;
     KVHP_TRY(rows_workspace(m, B, max_seq_len, static_cast<hipStream_t>(s), &ws, &ws_bytes));
+    if (B > 1 && B <= 32 && m.rows_ok && !m.tiled)
+        KVHP_TRY(build_tiled(m, static_cast<hipStream_t>(s)));
     KVHP_TRY(kvhp_embedding(tokens, m.embed, m.hidden, B, H, c.vocab_size, s));
     if (B == 1) {
         // one sequence: the batch-1 step's GEMV kernels (no padded MFMA columns)
@@ -402,9 +443,10 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
     }
     if (B <= 32 && m.rows_ok) {
         // Skinny-GEMM projections with the batch-1 step's fusions: every
-        // weight read once per step for all B rows, six launches per layer
-        // (seven when the down projection's x is large enough to split over
-        // K: its partials live in the model's own buffer).
+        // weight read once per step for all B rows, from its tiled copy, six
+        // launches per layer (seven when the down projection's x is large
+        // enough to split over K: its partials live in the model's own
+        // buffer).
         const size_t part_need = kvhp_gemv_rows_workspace_bytes(H, F, B);
         if (part_need > m.part_rows_bytes) {
             char* p = static_cast<char*>(m.part_rows);
@@ -414,21 +456,23 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
         }
         for (int l = 0; l < c.num_layers; ++l) {
             const Layer& L = m.layers[l];
-            KVHP_TRY(kvhp_rmsnorm_qkv_rope_append_rows(
-                L.w_qkv, m.hidden, L.attn_norm, c.rms_eps, positions, c.rope_theta, m.q,
+            KVHP_TRY(kvhp_rmsnorm_qkv_rope_append_rows_tiled(
+                L.w_qkv_t, m.hidden, L.attn_norm, c.rms_eps, positions, c.rope_theta, m.q,
                 layer_pool(m, pg, l, 0), layer_pool(m, pg, l, 1), wbt, pg.max_pages,
                 pg.num_pages, Hq, Hkv, D, H, B, s));
             const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
             KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, seq_lens, m.attn, B, Hq, Hkv, D,
                                            max_seq_len, 0, ws, ws_bytes, s));
-            KVHP_TRY(kvhp_gemv_residual_rows(L.w_o, m.attn, m.hidden, m.hidden, H, Hq * D, B, s));
-            KVHP_TRY(kvhp_rmsnorm_gemv_swiglu_rows(L.w_gate_up, m.hidden, L.ffn_norm, c.rms_eps,
-                                                   m.act, F, H, B, s));
-            KVHP_TRY(kvhp_gemv_residual_rows_ws(L.w_down, m.act, m.hidden, m.hidden, H, F, B,
-                                                part_need ? m.part_rows : nullptr, part_need, s));
+            KVHP_TRY(kvhp_gemv_residual_rows_tiled(L.w_o_t, m.attn, m.hidden, m.hidden, H, Hq * D,
+                                                   B, nullptr, 0, s));
+            KVHP_TRY(kvhp_rmsnorm_gemv_swiglu_rows_tiled(L.w_gate_up_t, m.hidden, L.ffn_norm,
+                                                         c.rms_eps, m.act, F, H, B, s));
+            KVHP_TRY(kvhp_gemv_residual_rows_tiled(L.w_down_t, m.act, m.hidden, m.hidden, H, F,
+                                                   B, part_need ? m.part_rows : nullptr,
+                                                   part_need, s));
         }
-        KVHP_TRY(kvhp_rmsnorm_gemv_rows(m.lm_head, m.hidden, m.final_norm, c.rms_eps, nullptr,
-                                        logits, c.vocab_size, H, B, s));
+        KVHP_TRY(kvhp_rmsnorm_gemv_rows_tiled(m.lm_head_t, m.hidden, m.final_norm, c.rms_eps,
+                                              nullptr, logits, c.vocab_size, H, B, s));
         return kvhp_argmax_rows(logits, B, c.vocab_size, next, s);
     }
     for (int l = 0; l < c.num_layers; ++l) {
@@ -843,6 +887,12 @@ extern "C" int kvhp_llama_reserve(void* model, int max_batch, int max_seq_len) {
         char* p = static_cast<char*>(m.part_rows);
         KVHP_TRY(regrow(m, &p, &m.part_rows_bytes, part_need, nullptr, "llama_reserve"));
         m.part_rows = p;
+    }
+    if (max_batch > 1 && m.rows_ok) {
+        // the batched projections' tiled weights, from the weights as they
+        // are now
+        KVHP_TRY(build_tiled(m, m.stream));
+        KVHP_HIP(hipStreamSynchronize(m.stream), "hipStreamSynchronize(llama_reserve)");
     }
     return KVHP_OK;
 }

@@ -400,6 +400,8 @@ __device__ __forceinline__ void lds_barrier() {
 // first, so the operand is fp16(x * rs * w) as the batch-1 kernel rounds it.
 struct RowsArgs {
     const f16* W;          // [rows][K]
+    const f16* Wt;         // the same weights tiled (rows_tile_kernel), or null: loads
+                           // then read 1 KB contiguous per wave and k step
     const f16* x;          // [B][K]
     const f16* norm_w;     // [K] RMSNorm weight, or null
     float eps;
@@ -477,7 +479,15 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
         }
         const f16* wp = a.W + (int64_t)row * a.K + ks;
         // lanes past the live rows load nothing (their output rows are dropped)
-        if (col < L) {
+        if (col < L && a.Wt) {
+            // tiled: 16-row tiles (paired epilogues always run 16 live rows on
+            // them); 8 live rows are half h of tile tile/2 (plain rows only)
+            const int t16 = L == 16 ? tile : tile >> 1;
+            const int l = L == 16 ? lane : 16 * g + 8 * (tile & 1) + col;
+            const f16* tp = a.Wt + (((int64_t)t16 * (a.K / 32) + sl * C) * kWave + l) * 8;
+#pragma unroll
+            for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(tp + t * kWave * 8);
+        } else if (col < L) {
 #pragma unroll
             for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(wp + 32 * t);
         } else {
@@ -794,6 +804,7 @@ int launch_rows(RowsArgs a, hipStream_t s, const char* what) {
             return (a.N + live - 1) / live;
     };
     a.live = tiles_for(16) < kNumCUs && tiles_for(8) <= kNumCUs ? 8 : 16;
+    if (a.Wt && (EPI == kEpiSwiglu || EPI == kEpiQKV)) a.live = 16;   // the tiles' row pairing
     a.tiles = tiles_for(a.live);
     if (C == 8) {
         launch_rows_c<8, 8, EPI, RMS>(a, NW, s);
@@ -831,10 +842,17 @@ __global__ void __launch_bounds__(kWave * kWpg) ksplit_partial_kernel(const Rows
 
     // this wave's weight tile first (streamed once; rows past N repeat row N-1)
     half8 wr[C];
-    const int row = min(tile * 16 + col, a.N - 1);
-    const f16* wp = a.W + (int64_t)row * a.K + k0 + 8 * g;
+    if (a.Wt) {   // tiled: tiles past the last (their outputs dropped) re-read it
+        const int t16 = min(tile, (a.N + 15) / 16 - 1);
+        const f16* tp = a.Wt + (((int64_t)t16 * (a.K / 32) + slice * C) * kWave + lane) * 8;
 #pragma unroll
-    for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(wp + 32 * t);
+        for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(tp + t * kWave * 8);
+    } else {
+        const int row = min(tile * 16 + col, a.N - 1);
+        const f16* wp = a.W + (int64_t)row * a.K + k0 + 8 * g;
+#pragma unroll
+        for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(wp + 32 * t);
+    }
     // x slice of every batch row, zero past B
     for (int i = static_cast<int>(threadIdx.x); i < NBT * 16 * 4 * C; i += kWave * kWpg) {
         const int r = i / (4 * C), ch = i % (4 * C);   // ch = 4t + k group
@@ -916,6 +934,55 @@ int launch_ksplit_residual(const RowsArgs& a, float* part, hipStream_t s, const 
     hipLaunchKernelGGL(ksplit_reduce_residual_kernel, dim3((unsigned)((threads + 127) / 128)),
                        dim3(128), 0, s, a, part, NW);
     return check_launch(what);
+}
+
+// ---- Tiled weights for the batched projections --------------------------------
+// Tile T holds the 16 rows gemm_rows_kernel maps to lanes col = 0..15 of a
+// 16-live-row tile -- plain: row 16T + col; SwiGLU: gate row n = 8T + col % 8
+// (col < 8) and its up row N + n (col >= 8); QKV: dims d0 .. d0+7 of head
+// T / (D/16) (col < 8) and their RoPE partners d0 + D/2 .. (col >= 8), d0 =
+// 8 (T % (D/16)) -- and stores k step s (k = 32s .. 32s+31) of lane l = 16g +
+// col, W[row][32s + 8g .. +8], as the 16 bytes at ((T * K/32 + s) * 64 + l) * 8
+// halfs.  A wave's load of one k step is then 1 KB contiguous and a tile 32K
+// bytes; row-major loads of the same operands (16 rows of 64 bytes, 4 KB
+// apart, per instruction) streamed the gate/up weights at 4.2 TB/s against
+// 6.0 TB/s tiled.  Rows past the matrix repeat its last row (those outputs
+// are dropped), so the kernels' arithmetic and results are unchanged.
+__device__ __forceinline__ int tiled_row(int kind, int N, int D, int T, int col) {
+    if (kind == KVHP_ROWS_QKV) {
+        const int tph = D / 16, d0 = 8 * (T % tph);
+        return (T / tph) * D + (col < 8 ? 0 : D / 2) + d0 + (col & 7);
+    }
+    if (kind == KVHP_ROWS_SWIGLU) {
+        const int n = min(8 * T + (col & 7), N - 1);
+        return col < 8 ? n : N + n;
+    }
+    return min(16 * T + col, N - 1);
+}
+
+__global__ void __launch_bounds__(256) rows_tile_kernel(const f16* W, f16* Wt, int kind, int N,
+                                                        int K, int D, int64_t chunks) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= chunks) return;
+    const int l = static_cast<int>(i % kWave);
+    const int64_t ts = i / kWave;
+    const int s = static_cast<int>(ts % (K / 32));
+    const int T = static_cast<int>(ts / (K / 32));
+    const int row = tiled_row(kind, N, D, T, l & 15);
+    store_half8(Wt + i * 8, load_half8(W + (int64_t)row * K + 32 * s + 8 * (l >> 4)));
+}
+
+// 16-row tiles of a tiled matrix (as gemm_rows_kernel counts them at 16 live
+// rows); 0 for unsupported shapes.
+int64_t rows_tiles(int kind, int N, int K, int Hq, int Hkv, int D) {
+    int C = 0, NW = 0;
+    if (K <= 0 || !rows_shape(K, C, NW)) return 0;
+    if (kind == KVHP_ROWS_QKV)
+        return Hq > 0 && Hkv > 0 && D > 0 && D % 16 == 0 ? (int64_t)(Hq + 2 * Hkv) * (D / 16) : 0;
+    if (N <= 0) return 0;
+    if (kind == KVHP_ROWS_SWIGLU) return (N + 7) / 8;
+    if (kind == KVHP_ROWS_PLAIN) return (N + 15) / 16;
+    return 0;
 }
 
 // Row-wise RMSNorm (prefill): one workgroup of 256 threads per row.
@@ -1275,15 +1342,16 @@ int rmsnorm_qkv_rope_append_at(const void* W_qkv, const void* x, const void* nor
 }
 }  // namespace kvhp
 
-extern "C" int kvhp_gemv_residual_rows(const void* W, const void* x, const void* r, void* y,
-                                       int N, int K, int batch, void* stream) {
-    clear_error();
+int residual_rows_impl(const void* W, const void* Wt, const void* x, const void* r, void* y,
+                       int N, int K, int batch, void* workspace, size_t workspace_bytes,
+                       hipStream_t s, const char* what) {
     if (N == 0 || batch == 0) return KVHP_OK;
-    int rc = check_gemv(W, x, N, K, "gemv_residual_rows");
+    int rc = check_gemv(W ? W : Wt, x, N, K, what);
     if (rc) return rc;
-    KVHP_REQUIRE(r && y, KVHP_ERR_INVALID, "gemv_residual_rows: null residual/output");
+    KVHP_REQUIRE(r && y, KVHP_ERR_INVALID, "%s: null residual/output", what);
     RowsArgs a{};
     a.W = static_cast<const f16*>(W);
+    a.Wt = static_cast<const f16*>(Wt);
     a.x = static_cast<const f16*>(x);
     a.N = N;
     a.K = K;
@@ -1291,8 +1359,20 @@ extern "C" int kvhp_gemv_residual_rows(const void* W, const void* x, const void*
     a.resid = static_cast<const f16*>(r);
     a.y16 = static_cast<f16*>(y);
     a.ldy = N;
-    return launch_rows<kEpiResidual, false>(a, static_cast<hipStream_t>(stream),
-                                               "gemv_residual_rows");
+    const size_t need = ksplit_bytes(N, K, batch);
+    if (need == 0 || workspace == nullptr) return launch_rows<kEpiResidual, false>(a, s, what);
+    KVHP_REQUIRE(workspace_bytes >= need, KVHP_ERR_WORKSPACE,
+                 "%s: workspace of %zu bytes, this call needs %zu", what, workspace_bytes, need);
+    KVHP_REQUIRE(aligned16(W ? W : Wt) && aligned16(x) && aligned16(workspace),
+                 KVHP_ERR_UNSUPPORTED, "%s: W, x and the workspace must be 16-byte aligned", what);
+    return launch_ksplit_residual(a, static_cast<float*>(workspace), s, what);
+}
+
+extern "C" int kvhp_gemv_residual_rows(const void* W, const void* x, const void* r, void* y,
+                                       int N, int K, int batch, void* stream) {
+    clear_error();
+    return residual_rows_impl(W, nullptr, x, r, y, N, K, batch, nullptr, 0,
+                              static_cast<hipStream_t>(stream), "gemv_residual_rows");
 }
 
 extern "C" size_t kvhp_gemv_rows_workspace_bytes(int N, int K, int batch) {
@@ -1303,43 +1383,32 @@ extern "C" int kvhp_gemv_residual_rows_ws(const void* W, const void* x, const vo
                                           int N, int K, int batch, void* workspace,
                                           size_t workspace_bytes, void* stream) {
     clear_error();
-    if (N == 0 || batch == 0) return KVHP_OK;
-    const size_t need = ksplit_bytes(N, K, batch);
-    if (need == 0 || workspace == nullptr)
-        return kvhp_gemv_residual_rows(W, x, r, y, N, K, batch, stream);
-    int rc = check_gemv(W, x, N, K, "gemv_residual_rows_ws");
-    if (rc) return rc;
-    KVHP_REQUIRE(r && y, KVHP_ERR_INVALID, "gemv_residual_rows_ws: null residual/output");
-    KVHP_REQUIRE(workspace_bytes >= need, KVHP_ERR_WORKSPACE,
-                 "gemv_residual_rows_ws: workspace of %zu bytes, this call needs %zu",
-                 workspace_bytes, need);
-    KVHP_REQUIRE(aligned16(W) && aligned16(x) && aligned16(workspace), KVHP_ERR_UNSUPPORTED,
-                 "gemv_residual_rows_ws: W, x and the workspace must be 16-byte aligned");
-    RowsArgs a{};
-    a.W = static_cast<const f16*>(W);
-    a.x = static_cast<const f16*>(x);
-    a.N = N;
-    a.K = K;
-    a.B = batch;
-    a.resid = static_cast<const f16*>(r);
-    a.y16 = static_cast<f16*>(y);
-    a.ldy = N;
-    return launch_ksplit_residual(a, static_cast<float*>(workspace),
-                                  static_cast<hipStream_t>(stream), "gemv_residual_rows_ws");
+    return residual_rows_impl(W, nullptr, x, r, y, N, K, batch, workspace, workspace_bytes,
+                              static_cast<hipStream_t>(stream), "gemv_residual_rows_ws");
 }
 
-extern "C" int kvhp_rmsnorm_gemv_rows(const void* W, const void* x, const void* norm_w, float eps,
-                                      void* y16, float* y32, int N, int K, int batch,
-                                      void* stream) {
+extern "C" int kvhp_gemv_residual_rows_tiled(const void* W_tiled, const void* x, const void* r,
+                                             void* y, int N, int K, int batch, void* workspace,
+                                             size_t workspace_bytes, void* stream) {
     clear_error();
+    KVHP_REQUIRE(W_tiled, KVHP_ERR_INVALID, "gemv_residual_rows_tiled: null weights");
+    return residual_rows_impl(nullptr, W_tiled, x, r, y, N, K, batch, workspace,
+                              workspace_bytes, static_cast<hipStream_t>(stream),
+                              "gemv_residual_rows_tiled");
+}
+
+int rmsnorm_rows_impl(const void* W, const void* Wt, const void* x, const void* norm_w,
+                      float eps, void* y16, float* y32, int N, int K, int batch, hipStream_t s,
+                      const char* what) {
     if (N == 0 || batch == 0) return KVHP_OK;
-    int rc = check_gemv(W, x, N, K, "rmsnorm_gemv_rows");
+    int rc = check_gemv(W ? W : Wt, x, N, K, what);
     if (rc) return rc;
-    KVHP_REQUIRE(norm_w, KVHP_ERR_INVALID, "rmsnorm_gemv_rows: null norm weight");
+    KVHP_REQUIRE(norm_w, KVHP_ERR_INVALID, "%s: null norm weight", what);
     KVHP_REQUIRE((y16 != nullptr) != (y32 != nullptr), KVHP_ERR_INVALID,
-                 "rmsnorm_gemv_rows: give exactly one of y16 / y32");
+                 "%s: give exactly one of y16 / y32", what);
     RowsArgs a{};
     a.W = static_cast<const f16*>(W);
+    a.Wt = static_cast<const f16*>(Wt);
     a.x = static_cast<const f16*>(x);
     a.norm_w = static_cast<const f16*>(norm_w);
     a.eps = eps;
@@ -1349,21 +1418,35 @@ extern "C" int kvhp_rmsnorm_gemv_rows(const void* W, const void* x, const void* 
     a.y16 = static_cast<f16*>(y16);
     a.y32 = y32;
     a.ldy = N;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    return y32 ? launch_rows<kEpiF32, true>(a, s, "rmsnorm_gemv_rows")
-               : launch_rows<kEpiF16, true>(a, s, "rmsnorm_gemv_rows");
+    return y32 ? launch_rows<kEpiF32, true>(a, s, what) : launch_rows<kEpiF16, true>(a, s, what);
 }
 
-extern "C" int kvhp_rmsnorm_gemv_swiglu_rows(const void* W_gate_up, const void* x,
-                                             const void* norm_w, float eps, void* out, int N,
-                                             int K, int batch, void* stream) {
+extern "C" int kvhp_rmsnorm_gemv_rows(const void* W, const void* x, const void* norm_w, float eps,
+                                      void* y16, float* y32, int N, int K, int batch,
+                                      void* stream) {
     clear_error();
+    return rmsnorm_rows_impl(W, nullptr, x, norm_w, eps, y16, y32, N, K, batch,
+                             static_cast<hipStream_t>(stream), "rmsnorm_gemv_rows");
+}
+
+extern "C" int kvhp_rmsnorm_gemv_rows_tiled(const void* W_tiled, const void* x,
+                                            const void* norm_w, float eps, void* y16, float* y32,
+                                            int N, int K, int batch, void* stream) {
+    clear_error();
+    KVHP_REQUIRE(W_tiled, KVHP_ERR_INVALID, "rmsnorm_gemv_rows_tiled: null weights");
+    return rmsnorm_rows_impl(nullptr, W_tiled, x, norm_w, eps, y16, y32, N, K, batch,
+                             static_cast<hipStream_t>(stream), "rmsnorm_gemv_rows_tiled");
+}
+
+int swiglu_rows_impl(const void* W, const void* Wt, const void* x, const void* norm_w, float eps,
+                     void* out, int N, int K, int batch, hipStream_t s, const char* what) {
     if (N == 0 || batch == 0) return KVHP_OK;
-    int rc = check_gemv(W_gate_up, x, N, K, "rmsnorm_gemv_swiglu_rows");
+    int rc = check_gemv(W ? W : Wt, x, N, K, what);
     if (rc) return rc;
-    KVHP_REQUIRE(norm_w && out, KVHP_ERR_INVALID, "rmsnorm_gemv_swiglu_rows: null pointer");
+    KVHP_REQUIRE(norm_w && out, KVHP_ERR_INVALID, "%s: null pointer", what);
     RowsArgs a{};
-    a.W = static_cast<const f16*>(W_gate_up);
+    a.W = static_cast<const f16*>(W);
+    a.Wt = static_cast<const f16*>(Wt);
     a.x = static_cast<const f16*>(x);
     a.norm_w = static_cast<const f16*>(norm_w);
     a.eps = eps;
@@ -1372,29 +1455,43 @@ extern "C" int kvhp_rmsnorm_gemv_swiglu_rows(const void* W_gate_up, const void* 
     a.B = batch;
     a.y16 = static_cast<f16*>(out);
     a.ldy = N;
-    return launch_rows<kEpiSwiglu, true>(a, static_cast<hipStream_t>(stream),
-                                            "rmsnorm_gemv_swiglu_rows");
+    return launch_rows<kEpiSwiglu, true>(a, s, what);
 }
 
-extern "C" int kvhp_rmsnorm_qkv_rope_append_rows(
-    const void* W_qkv, const void* x, const void* norm_w, float eps, const int32_t* positions,
-    float rope_theta, void* q_out, void* pool_k, void* pool_v, const int32_t* block_tables,
-    int max_pages, int num_pages, int num_q_heads, int num_kv_heads, int head_dim, int K,
-    int batch, void* stream) {
+extern "C" int kvhp_rmsnorm_gemv_swiglu_rows(const void* W_gate_up, const void* x,
+                                             const void* norm_w, float eps, void* out, int N,
+                                             int K, int batch, void* stream) {
     clear_error();
+    return swiglu_rows_impl(W_gate_up, nullptr, x, norm_w, eps, out, N, K, batch,
+                            static_cast<hipStream_t>(stream), "rmsnorm_gemv_swiglu_rows");
+}
+
+extern "C" int kvhp_rmsnorm_gemv_swiglu_rows_tiled(const void* W_tiled, const void* x,
+                                                   const void* norm_w, float eps, void* out, int N,
+                                                   int K, int batch, void* stream) {
+    clear_error();
+    KVHP_REQUIRE(W_tiled, KVHP_ERR_INVALID, "rmsnorm_gemv_swiglu_rows_tiled: null weights");
+    return swiglu_rows_impl(nullptr, W_tiled, x, norm_w, eps, out, N, K, batch,
+                            static_cast<hipStream_t>(stream), "rmsnorm_gemv_swiglu_rows_tiled");
+}
+
+int qkv_rows_impl(const void* W_qkv, const void* Wt, const void* x, const void* norm_w, float eps,
+                  const int32_t* positions, float rope_theta, void* q_out, void* pool_k,
+                  void* pool_v, const int32_t* block_tables, int max_pages, int num_pages,
+                  int num_q_heads, int num_kv_heads, int head_dim, int K, int batch,
+                  hipStream_t s, const char* what) {
     if (batch == 0) return KVHP_OK;
     const int N = (num_q_heads + 2 * num_kv_heads) * head_dim;
-    int rc = check_gemv(W_qkv, x, N, K, "rmsnorm_qkv_rope_append_rows");
+    int rc = check_gemv(W_qkv ? W_qkv : Wt, x, N, K, what);
     if (rc) return rc;
     KVHP_REQUIRE(norm_w && positions && q_out && pool_k && pool_v && block_tables,
-                 KVHP_ERR_INVALID, "rmsnorm_qkv_rope_append_rows: null pointer");
+                 KVHP_ERR_INVALID, "%s: null pointer", what);
     KVHP_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 16 == 0,
-                 KVHP_ERR_INVALID,
-                 "rmsnorm_qkv_rope_append_rows: head_dim %d must be a multiple of 16", head_dim);
-    KVHP_REQUIRE(max_pages > 0 && num_pages > 0, KVHP_ERR_INVALID,
-                 "rmsnorm_qkv_rope_append_rows: empty page pool");
+                 KVHP_ERR_INVALID, "%s: head_dim %d must be a multiple of 16", what, head_dim);
+    KVHP_REQUIRE(max_pages > 0 && num_pages > 0, KVHP_ERR_INVALID, "%s: empty page pool", what);
     RowsArgs a{};
     a.W = static_cast<const f16*>(W_qkv);
+    a.Wt = static_cast<const f16*>(Wt);
     a.x = static_cast<const f16*>(x);
     a.norm_w = static_cast<const f16*>(norm_w);
     a.eps = eps;
@@ -1413,8 +1510,57 @@ extern "C" int kvhp_rmsnorm_qkv_rope_append_rows(
     a.bt = block_tables;
     a.max_pages = max_pages;
     a.num_pages = num_pages;
-    return launch_rows<kEpiQKV, true>(a, static_cast<hipStream_t>(stream),
-                                         "rmsnorm_qkv_rope_append_rows");
+    return launch_rows<kEpiQKV, true>(a, s, what);
+}
+
+extern "C" int kvhp_rmsnorm_qkv_rope_append_rows(
+    const void* W_qkv, const void* x, const void* norm_w, float eps, const int32_t* positions,
+    float rope_theta, void* q_out, void* pool_k, void* pool_v, const int32_t* block_tables,
+    int max_pages, int num_pages, int num_q_heads, int num_kv_heads, int head_dim, int K,
+    int batch, void* stream) {
+    clear_error();
+    return qkv_rows_impl(W_qkv, nullptr, x, norm_w, eps, positions, rope_theta, q_out, pool_k,
+                         pool_v, block_tables, max_pages, num_pages, num_q_heads, num_kv_heads,
+                         head_dim, K, batch, static_cast<hipStream_t>(stream),
+                         "rmsnorm_qkv_rope_append_rows");
+}
+
+extern "C" int kvhp_rmsnorm_qkv_rope_append_rows_tiled(
+    const void* W_tiled, const void* x, const void* norm_w, float eps, const int32_t* positions,
+    float rope_theta, void* q_out, void* pool_k, void* pool_v, const int32_t* block_tables,
+    int max_pages, int num_pages, int num_q_heads, int num_kv_heads, int head_dim, int K,
+    int batch, void* stream) {
+    clear_error();
+    KVHP_REQUIRE(W_tiled, KVHP_ERR_INVALID, "rmsnorm_qkv_rope_append_rows_tiled: null weights");
+    return qkv_rows_impl(nullptr, W_tiled, x, norm_w, eps, positions, rope_theta, q_out, pool_k,
+                         pool_v, block_tables, max_pages, num_pages, num_q_heads, num_kv_heads,
+                         head_dim, K, batch, static_cast<hipStream_t>(stream),
+                         "rmsnorm_qkv_rope_append_rows_tiled");
+}
+
+extern "C" size_t kvhp_rows_tiled_bytes(int kind, int N, int K, int num_q_heads,
+                                        int num_kv_heads, int head_dim) {
+    return static_cast<size_t>(rows_tiles(kind, N, K, num_q_heads, num_kv_heads, head_dim)) *
+           32 * static_cast<size_t>(K > 0 ? K : 0);
+}
+
+extern "C" int kvhp_rows_tile_weights(int kind, const void* W, int N, int K, int num_q_heads,
+                                      int num_kv_heads, int head_dim, void* W_tiled,
+                                      void* stream) {
+    clear_error();
+    KVHP_REQUIRE(W && W_tiled, KVHP_ERR_INVALID, "rows_tile_weights: null pointer");
+    KVHP_REQUIRE(aligned16(W) && aligned16(W_tiled), KVHP_ERR_UNSUPPORTED,
+                 "rows_tile_weights: W and W_tiled must be 16-byte aligned");
+    const int64_t tiles = rows_tiles(kind, N, K, num_q_heads, num_kv_heads, head_dim);
+    KVHP_REQUIRE(tiles > 0, KVHP_ERR_UNSUPPORTED,
+                 "rows_tile_weights: kind %d, N=%d, K=%d (heads %d/%d of %d) is not a shape the "
+                 "batched projections take", kind, N, K, num_q_heads, num_kv_heads, head_dim);
+    if (kind == KVHP_ROWS_QKV) N = (num_q_heads + 2 * num_kv_heads) * head_dim;
+    const int64_t chunks = tiles * (K / 32) * kWave;
+    hipLaunchKernelGGL(rows_tile_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)),
+                       dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<const f16*>(W),
+                       static_cast<f16*>(W_tiled), kind, N, K, head_dim, chunks);
+    return check_launch("rows_tile_weights");
 }
 
 extern "C" int kvhp_rmsnorm(const void* x, const void* weight, void* out, int64_t rows,

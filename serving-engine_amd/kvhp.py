@@ -103,6 +103,17 @@ _SIGNATURES = {
     "kvhp_rmsnorm_qkv_rope_append_rows": (_i32, [_vp, _vp, _vp, _f32, _vp, _f32, _vp, _vp, _vp,
                                                  _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                                  _vp]),
+    "kvhp_rows_tiled_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "kvhp_rows_tile_weights": (_i32, [_i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "kvhp_gemv_residual_rows_tiled": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _sz,
+                                             _vp]),
+    "kvhp_rmsnorm_gemv_rows_tiled": (_i32, [_vp, _vp, _vp, _f32, _vp, _vp, _i32, _i32, _i32,
+                                            _vp]),
+    "kvhp_rmsnorm_gemv_swiglu_rows_tiled": (_i32, [_vp, _vp, _vp, _f32, _vp, _i32, _i32, _i32,
+                                                   _vp]),
+    "kvhp_rmsnorm_qkv_rope_append_rows_tiled": (_i32, [_vp, _vp, _vp, _f32, _vp, _f32, _vp, _vp,
+                                                       _vp, _vp, _i32, _i32, _i32, _i32, _i32,
+                                                       _i32, _i32, _vp]),
     "kvhp_rmsnorm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
     "kvhp_apply_rope": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp]),
     "kvhp_split_qkv_rope": (_i32, [_vp, _i64, _i32, _i32, _i32, _i64, _f32, _vp, _vp, _vp, _vp]),
@@ -419,6 +430,46 @@ def rmsnorm_qkv_rope_append_rows(W_qkv, x, norm_w, eps, positions, theta, q_out,
     """pool_k / pool_v [Hkv][P][16][D]; block_tables int32 [batch][max_pages]."""
     _check(load().kvhp_rmsnorm_qkv_rope_append_rows(
         _ptr(W_qkv), _ptr(x), _ptr(norm_w), eps, _ptr(positions), theta, _ptr(q_out),
+        _ptr(pool_k), _ptr(pool_v), _ptr(block_tables), block_tables.shape[1], pool_k.shape[1],
+        num_q_heads, num_kv_heads, head_dim, K, batch, _stream(stream)))
+
+
+ROWS_PLAIN, ROWS_SWIGLU, ROWS_QKV = 0, 1, 2
+
+
+def rows_tiled_bytes(kind, N, K, num_q_heads=0, num_kv_heads=0, head_dim=0):
+    return load().kvhp_rows_tiled_bytes(kind, N, K, num_q_heads, num_kv_heads, head_dim)
+
+
+def rows_tile_weights(kind, W, N, K, W_tiled, num_q_heads=0, num_kv_heads=0, head_dim=0,
+                      stream=None):
+    """Copy row-major W into the batched projections' tiled layout (W_tiled:
+    rows_tiled_bytes bytes, any dtype)."""
+    _check(load().kvhp_rows_tile_weights(kind, _ptr(W), N, K, num_q_heads, num_kv_heads,
+                                         head_dim, _ptr(W_tiled), _stream(stream)))
+
+
+def gemv_residual_rows_tiled(Wt, x, r, y, N, K, batch, workspace=None, stream=None):
+    nbytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(load().kvhp_gemv_residual_rows_tiled(_ptr(Wt), _ptr(x), _ptr(r), _ptr(y), N, K, batch,
+                                                _ptr(workspace), nbytes, _stream(stream)))
+
+
+def rmsnorm_gemv_rows_tiled(Wt, x, norm_w, eps, N, K, batch, y16=None, y32=None, stream=None):
+    _check(load().kvhp_rmsnorm_gemv_rows_tiled(_ptr(Wt), _ptr(x), _ptr(norm_w), eps, _ptr(y16),
+                                               _ptr(y32), N, K, batch, _stream(stream)))
+
+
+def rmsnorm_gemv_swiglu_rows_tiled(Wt, x, norm_w, eps, out, N, K, batch, stream=None):
+    _check(load().kvhp_rmsnorm_gemv_swiglu_rows_tiled(_ptr(Wt), _ptr(x), _ptr(norm_w), eps,
+                                                      _ptr(out), N, K, batch, _stream(stream)))
+
+
+def rmsnorm_qkv_rope_append_rows_tiled(Wt, x, norm_w, eps, positions, theta, q_out, pool_k,
+                                       pool_v, block_tables, num_q_heads, num_kv_heads, head_dim,
+                                       K, batch, stream=None):
+    _check(load().kvhp_rmsnorm_qkv_rope_append_rows_tiled(
+        _ptr(Wt), _ptr(x), _ptr(norm_w), eps, _ptr(positions), theta, _ptr(q_out),
         _ptr(pool_k), _ptr(pool_v), _ptr(block_tables), block_tables.shape[1], pool_k.shape[1],
         num_q_heads, num_kv_heads, head_dim, K, batch, _stream(stream)))
 

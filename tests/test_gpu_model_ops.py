@@ -261,6 +261,113 @@ def test_rmsnorm_qkv_rope_append_rows(batch, hq, hkv, d, k):
     assert not pk[:, ~written].any() and not pv[:, ~written].any()
 
 
+def _tiled(kind, W, n, k, hq=0, hkv=0, d=0):
+    nb = kvhp.rows_tiled_bytes(kind, n, k, hq, hkv, d)
+    tiles = {kvhp.ROWS_QKV: (hq + 2 * hkv) * d // 16 if d else 0,
+             kvhp.ROWS_SWIGLU: (n + 7) // 8, kvhp.ROWS_PLAIN: (n + 15) // 16}[kind]
+    assert nb == tiles * 32 * k
+    Wt = torch.full((nb // 2,), float("nan"), dtype=torch.float16, device="cuda")
+    kvhp.rows_tile_weights(kind, W, n, k, Wt, hq, hkv, d)
+    return Wt
+
+
+@pytest.mark.parametrize("batch", [1, 2, 8, 17, 32])
+def test_rows_tiled_plain_bit_identical(batch):
+    """Weights pre-tiled for the batched projections give bit-identical
+    outputs to the row-major calls: residual (8 live rows per tile at N =
+    2048, 16 at N = 4096, clamped rows at N = 77), the K-split residual
+    (K = 5632, B >= 15) and the fp16 / fp32 RMSNorm projections (the LM-head
+    shape included)."""
+    rng = np.random.default_rng(300 + batch)
+    for n, k in [(2048, 2048), (4096, 2048), (77, 512), (2048, 5632)]:
+        W = to_gpu(oracle.normal_f16(rng, (n, k), 0.02))
+        x = to_gpu(oracle.normal_f16(rng, (batch, k)))
+        r = oracle.normal_f16(rng, (batch, n))
+        Wt = _tiled(kvhp.ROWS_PLAIN, W, n, k)
+        y1, y2 = to_gpu(r), to_gpu(r)
+        kvhp.gemv_residual_rows(W, x, y1, y1, n, k, batch)
+        kvhp.gemv_residual_rows_tiled(Wt, x, y2, y2, n, k, batch)
+        need = kvhp.gemv_rows_workspace_bytes(n, k, batch)
+        ws = torch.full((max(need, 16),), 0xFF, dtype=torch.uint8, device="cuda")
+        y3, y4 = to_gpu(r), to_gpu(r)
+        kvhp.gemv_residual_rows_ws(W, x, y3, y3, n, k, batch, ws)
+        kvhp.gemv_residual_rows_tiled(Wt, x, y4, y4, n, k, batch, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), f"residual B={batch} {n}x{k}"
+        assert torch.equal(y3, y4), f"residual (workspace {need} B) B={batch} {n}x{k}"
+    for n, k in [(32000, 2048), (100, 768)]:
+        W = to_gpu(oracle.normal_f16(rng, (n, k), 0.02))
+        x = to_gpu(oracle.normal_f16(rng, (batch, k), 3.0))
+        w = to_gpu((1.0 + oracle.normal_f16(rng, (k,), 0.1).astype(np.float32)).astype(np.float16))
+        Wt = _tiled(kvhp.ROWS_PLAIN, W, n, k)
+        for dt in (torch.float32, torch.float16):
+            a = torch.empty((batch, n), dtype=dt, device="cuda")
+            b = torch.empty_like(a)
+            kw = "y32" if dt == torch.float32 else "y16"
+            kvhp.rmsnorm_gemv_rows(W, x, w, 1e-5, n, k, batch, **{kw: a})
+            kvhp.rmsnorm_gemv_rows_tiled(Wt, x, w, 1e-5, n, k, batch, **{kw: b})
+            torch.cuda.synchronize()
+            assert torch.equal(a, b), f"rmsnorm_gemv_rows {dt} B={batch} {n}x{k}"
+
+
+@pytest.mark.parametrize("batch", [1, 3, 8, 32])
+def test_rows_tiled_swiglu_and_qkv_bit_identical(batch):
+    """SwiGLU (gate/up rows paired inside a tile; N = 37 runs 8 live rows
+    row-major but 16 tiled) and the fused QKV + RoPE + page append (RoPE
+    dimension pairs inside a tile; D = 64, 128, 32) on tiled weights match
+    the row-major calls bit for bit, including the pages written and an idle
+    row."""
+    rng = np.random.default_rng(400 + batch)
+    for n, k in [(5632, 2048), (37, 2048), (100, 768)]:
+        Wgu = to_gpu(oracle.normal_f16(rng, (2 * n, k), 0.02))
+        x = to_gpu(oracle.normal_f16(rng, (batch, k)))
+        w = to_gpu((1.0 + oracle.normal_f16(rng, (k,), 0.1).astype(np.float32)).astype(np.float16))
+        Wt = _tiled(kvhp.ROWS_SWIGLU, Wgu, n, k)
+        a = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+        b = torch.empty_like(a)
+        kvhp.rmsnorm_gemv_swiglu_rows(Wgu, x, w, 1e-5, a, n, k, batch)
+        kvhp.rmsnorm_gemv_swiglu_rows_tiled(Wt, x, w, 1e-5, b, n, k, batch)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"swiglu B={batch} {n}x{k}"
+    for hq, hkv, d, k in [(32, 4, 64, 2048), (8, 2, 128, 2048), (4, 4, 32, 256)]:
+        n = (hq + 2 * hkv) * d
+        W = to_gpu(oracle.normal_f16(rng, (n, k), 0.02))
+        x = to_gpu(oracle.normal_f16(rng, (batch, k)))
+        w = to_gpu((1.0 + oracle.normal_f16(rng, (k,), 0.1).astype(np.float32)).astype(np.float16))
+        Wt = _tiled(kvhp.ROWS_QKV, W, 0, k, hq, hkv, d)
+        max_pages, P = 4, 4 * batch + 3
+        tables = to_gpu(rng.permutation(P)[:4 * batch].astype(np.int32).reshape(batch, 4))
+        pos = rng.integers(0, 64, batch).astype(np.int32)
+        if batch > 1:
+            pos[1] = -1
+        pos = to_gpu(pos)
+        outs = []
+        for tiled in (False, True):
+            pk = torch.zeros((hkv, P, 16, d), dtype=torch.float16, device="cuda")
+            pv = torch.zeros_like(pk)
+            q = torch.empty((batch, hq * d), dtype=torch.float16, device="cuda")
+            fn = kvhp.rmsnorm_qkv_rope_append_rows_tiled if tiled else \
+                kvhp.rmsnorm_qkv_rope_append_rows
+            fn(Wt if tiled else W, x, w, 1e-5, pos, 10000.0, q, pk, pv, tables, hq, hkv, d, k,
+               batch)
+            outs.append((q, pk, pv))
+        torch.cuda.synchronize()
+        for u, v, what in zip(outs[0], outs[1], ("q", "k pages", "v pages")):
+            assert torch.equal(u, v), f"qkv {what} B={batch} {hq}/{hkv}x{d}"
+
+
+def test_rows_tiled_errors():
+    W = torch.zeros((64, 1000), dtype=torch.float16, device="cuda")
+    Wt = torch.zeros((1 << 16,), dtype=torch.float16, device="cuda")
+    assert kvhp.rows_tiled_bytes(kvhp.ROWS_PLAIN, 64, 1000) == 0          # K not 256n / 352n
+    assert kvhp.rows_tiled_bytes(7, 64, 2048) == 0                        # unknown kind
+    assert kvhp.rows_tiled_bytes(kvhp.ROWS_QKV, 0, 2048, 4, 4, 24) == 0   # head_dim % 16
+    with pytest.raises(kvhp.KVHPError):
+        kvhp.rows_tile_weights(kvhp.ROWS_PLAIN, W, 64, 1000, Wt)
+    with pytest.raises(kvhp.KVHPError):
+        kvhp.gemv_residual_rows_tiled(None, W, W, W, 64, 2048, 2)
+
+
 def test_rows_projection_errors():
     W = torch.zeros((64, 2048), dtype=torch.float16, device="cuda")
     x = torch.zeros((40, 2048), dtype=torch.float16, device="cuda")
