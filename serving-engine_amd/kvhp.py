@@ -657,3 +657,21 @@ class LlamaModel:
         if rc != 0:
             raise KVHPError(KVHP_ERR_HIP, f"hipMemcpy device-to-host failed ({rc})")
         return out
+
+    def set_tensor(self, layer: int, which: int, values):
+        """Overwrite a model tensor from a host array of its element count
+        (synchronous).  Batched decode steps see the new weights after the
+        next reserve(), which rebuilds their tiled copies."""
+        np = self._np
+        ptr = ctypes.c_void_p()
+        n = ctypes.c_size_t()
+        _check(load().kvhp_llama_tensor(self._h, layer, which, ctypes.byref(ptr), ctypes.byref(n)))
+        src = np.ascontiguousarray(values, np.float16).reshape(-1)
+        if src.size != n.value:
+            raise KVHPError(KVHP_ERR_INVALID, f"tensor holds {n.value} elements, got {src.size}")
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipMemcpy.argtypes = [_vp, _vp, _sz, _i32]
+        hip.hipMemcpy.restype = _i32
+        rc = hip.hipMemcpy(ptr.value, src.ctypes.data, src.size * 2, 1)  # host to device
+        if rc != 0:
+            raise KVHPError(KVHP_ERR_HIP, f"hipMemcpy host-to-device failed ({rc})")

@@ -411,6 +411,61 @@ def test_decode_paged_graph_capture_needs_reserve():
     model.close()
 
 
+def test_batched_steps_see_rewritten_weights_after_reserve():
+    """Batched steps (2..32 rows) read the model's tiled copies of the four
+    projections and the LM head, built on the first batched step.  Weights
+    rewritten through kvhp_llama_tensor after that leave a batched step's
+    logits bit-identical to before (the copies are what the step reads);
+    after kvhp_llama_reserve rebuilds the copies, its logits equal those of
+    a fresh model that was given the same weights before its first batched
+    step, bit for bit, and differ from the old ones."""
+    cfg = _cfg(5632)
+    L, Hkv, D, V = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size
+    B, plen, max_pages = 6, 11, 2
+    P = B * max_pages
+    rng = np.random.default_rng(2718)
+    prompts = [rng.integers(0, V, plen).astype(np.int32) for _ in range(B)]
+    bt = torch.from_numpy(rng.permutation(P).astype(np.int32).reshape(B, max_pages)).cuda()
+    pos = torch.full((B,), plen, dtype=torch.int32, device="cuda")
+
+    def prefill(model):
+        pool = torch.zeros(L * 2 * Hkv * P * PAGE * D, dtype=torch.float16, device="cuda")
+        toks = [model.prefill_paged(prompts[b], pool, P, bt[b], max_pages)[0] for b in range(B)]
+        return pool, torch.tensor(toks, dtype=torch.int32, device="cuda")
+
+    def step(model, pool, toks):
+        lg = torch.empty(B, V, dtype=torch.float32, device="cuda")
+        nx = torch.empty(B, dtype=torch.int32, device="cuda")
+        model.decode_paged(toks, pool.clone(), P, bt, max_pages, pos, pos + 1, plen + 1, lg, nx)
+        torch.cuda.synchronize()
+        return lg.cpu().numpy()
+
+    # each kind of tiled tensor (in one layer or another) and the LM head,
+    # negated and scaled by 3/4; both models get the same fp16 values
+    edits = [(0, kvhp.LLAMA_W_QKV), (1, kvhp.LLAMA_W_O), (2, kvhp.LLAMA_W_GATE_UP),
+             (0, kvhp.LLAMA_W_DOWN), (-1, kvhp.LLAMA_LM_HEAD)]
+    model = kvhp.LlamaModel(cfg, seed=61, max_ctx=64)
+    pool, toks = prefill(model)
+    before = step(model, pool, toks)            # first batched step: builds the copies
+    new = {e: (model.tensor(*e).astype(np.float32) * -0.75).astype(np.float16) for e in edits}
+    for e in edits:
+        model.set_tensor(*e, new[e])
+    assert np.array_equal(step(model, pool, toks), before), "batched step read the new weights"
+    model.reserve(B, plen + 1)
+    after = step(model, pool, toks)
+
+    fresh = kvhp.LlamaModel(cfg, seed=61, max_ctx=64)
+    fpool, ftoks = prefill(fresh)
+    assert torch.equal(fpool, pool) and torch.equal(ftoks, toks)
+    for e in edits:
+        fresh.set_tensor(*e, new[e])
+    ref = step(fresh, fpool, ftoks)
+    assert np.array_equal(after, ref), "rebuilt copies differ from a fresh model's"
+    assert not np.array_equal(after, before)
+    fresh.close()
+    model.close()
+
+
 def test_paged_runner_argument_errors():
     cfg = _cfg()
     model = kvhp.LlamaModel(cfg, seed=3, max_ctx=32)
