@@ -51,6 +51,44 @@ int rmsnorm_qkv_rope_append_at(const void* W_qkv, const void* x, const void* nor
                                int max_pages, int num_pages, int num_q_heads, int num_kv_heads,
                                int head_dim, int K, hipStream_t stream);
 
+// Row-tiled activations: the batched runner keeps its hidden state and
+// SwiGLU output ([B][K], K % 32 == 0) in the lane order of the 16x16x32 MFMA
+// B operand, so that the batched projections load one k step of 16 batch
+// rows as 1 KB contiguous per wave instead of staging row-major rows through
+// LDS.  Element (b, k) sits at act_tiled_index(b, k,
+// nbt), nbt = ceil(B / 16) batch tiles: 1 KB block (k / 32, b / 16), lane
+// 16 (k % 32 / 8) + b % 16, element k % 8.  Eight consecutive k from a
+// multiple of 8 stay contiguous.  Rows past B inside the last tile are
+// padding (never read into a kept result).
+__host__ __device__ __forceinline__ int64_t act_tiled_index(int64_t b, int64_t k, int nbt) {
+    return ((((k >> 5) * nbt + (b >> 4)) * 64 + 16 * ((k & 31) >> 3) + (b & 15)) << 3) +
+           (k & 7);
+}
+inline int act_tiles_for(int batch) { return (batch + 15) / 16; }
+
+// The batched runner's entry points on row-tiled activations (act_tiles =
+// act_tiles_for(batch); 0: row-major, as the exported kvhp_* functions), in
+// model_ops.hip: the same kernels as kvhp_gemv_residual_rows_tiled /
+// kvhp_rmsnorm_gemv_rows_tiled / kvhp_rmsnorm_gemv_swiglu_rows_tiled /
+// kvhp_rmsnorm_qkv_rope_append_rows_tiled and kvhp_embedding, with x, the
+// residual and fp16 outputs in that layout (q, the pages and fp32 logits stay
+// as they are).  The residual projection takes the layouts of x and of the
+// residual stream separately: the attention output it reads stays row-major.
+int residual_rows_act(const void* Wt, const void* x, const void* r, void* y, int N, int K,
+                      int batch, void* workspace, size_t workspace_bytes, int x_tiles,
+                      int y_tiles, hipStream_t s);
+int rmsnorm_rows_act(const void* Wt, const void* x, const void* norm_w, float eps, void* y16,
+                     float* y32, int N, int K, int batch, int act_tiles, hipStream_t s);
+int swiglu_rows_act(const void* Wt, const void* x, const void* norm_w, float eps, void* out,
+                    int N, int K, int batch, int act_tiles, hipStream_t s);
+int qkv_rows_act(const void* Wt, const void* x, const void* norm_w, float eps,
+                 const int32_t* positions, float rope_theta, void* q_out, void* pool_k,
+                 void* pool_v, const int32_t* block_tables, int max_pages, int num_pages,
+                 int num_q_heads, int num_kv_heads, int head_dim, int K, int batch, int act_tiles,
+                 hipStream_t s);
+int embedding_act(const int32_t* token_ids, const void* table, void* out, int batch,
+                  int64_t hidden, int64_t vocab, int act_tiles, hipStream_t s);
+
 #define KVHP_REQUIRE(cond, code, ...)          \
     do {                                       \
         if (!(cond)) return ::kvhp::fail(code, __VA_ARGS__); \

@@ -97,6 +97,9 @@ struct Model {
     bool rows_ok = false;      // batched projections fit the skinny-GEMM kernels
     f16* lm_head_t = nullptr;  // LM head tiled for the batched kernels
     bool tiled = false;        // the tiled copies hold the current weights
+    // batched-step activations (2..32 rows), row-tiled (act_tiled_index):
+    // hidden [32][H], SwiGLU output [32][F]
+    f16 *hidden_t = nullptr, *act_t = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
 
@@ -398,6 +401,10 @@ int build_tiled(Model& m, hipStream_t s) {
         KVHP_TRY(tile(&L.w_down_t, KVHP_ROWS_PLAIN, L.w_down, H, F));
     }
     KVHP_TRY(tile(&m.lm_head_t, KVHP_ROWS_PLAIN, m.lm_head, c.vocab_size, H));
+    if (!m.hidden_t) {
+        KVHP_TRY(alloc_n(m, (size_t)32 * H, &m.hidden_t));
+        KVHP_TRY(alloc_n(m, (size_t)32 * F, &m.act_t));
+    }
     m.tiled = true;
     return KVHP_OK;
 }
@@ -419,7 +426,8 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
     KVHP_TRY(rows_workspace(m, B, max_seq_len, static_cast<hipStream_t>(s), &ws, &ws_bytes));
     if (B > 1 && B <= 32 && m.rows_ok && !m.tiled)
         KVHP_TRY(build_tiled(m, static_cast<hipStream_t>(s)));
-    KVHP_TRY(kvhp_embedding(tokens, m.embed, m.hidden, B, H, c.vocab_size, s));
+    if (B == 1 || B > 32 || !m.rows_ok)
+        KVHP_TRY(kvhp_embedding(tokens, m.embed, m.hidden, B, H, c.vocab_size, s));
     if (B == 1) {
         // one sequence: the batch-1 step's GEMV kernels (no padded MFMA columns)
         for (int l = 0; l < c.num_layers; ++l) {
@@ -446,7 +454,13 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
         // weight read once per step for all B rows, from its tiled copy, six
         // launches per layer (seven when the down projection's x is large
         // enough to split over K: its partials live in the model's own
-        // buffer).
+        // buffer).  The hidden state and the SwiGLU output stay row-tiled,
+        // so the projections that read them load x as 1 KB contiguous per
+        // wave and k step (bit-identical to row-major activations: the same
+        // operands); the attention output stays row-major (the o projection
+        // stages it through LDS as before).
+        const int nt = act_tiles_for(B);
+        const hipStream_t hs = static_cast<hipStream_t>(s);
         const size_t part_need = kvhp_gemv_rows_workspace_bytes(H, F, B);
         if (part_need > m.part_rows_bytes) {
             char* p = static_cast<char*>(m.part_rows);
@@ -454,25 +468,25 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                             "down-projection partials"));
             m.part_rows = p;
         }
+        KVHP_TRY(embedding_act(tokens, m.embed, m.hidden_t, B, H, c.vocab_size, nt, hs));
         for (int l = 0; l < c.num_layers; ++l) {
             const Layer& L = m.layers[l];
-            KVHP_TRY(kvhp_rmsnorm_qkv_rope_append_rows_tiled(
-                L.w_qkv_t, m.hidden, L.attn_norm, c.rms_eps, positions, c.rope_theta, m.q,
-                layer_pool(m, pg, l, 0), layer_pool(m, pg, l, 1), wbt, pg.max_pages,
-                pg.num_pages, Hq, Hkv, D, H, B, s));
+            KVHP_TRY(qkv_rows_act(L.w_qkv_t, m.hidden_t, L.attn_norm, c.rms_eps, positions,
+                                  c.rope_theta, m.q, layer_pool(m, pg, l, 0),
+                                  layer_pool(m, pg, l, 1), wbt, pg.max_pages, pg.num_pages, Hq,
+                                  Hkv, D, H, B, nt, hs));
             const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
             KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, seq_lens, m.attn, B, Hq, Hkv, D,
                                            max_seq_len, 0, ws, ws_bytes, s));
-            KVHP_TRY(kvhp_gemv_residual_rows_tiled(L.w_o_t, m.attn, m.hidden, m.hidden, H, Hq * D,
-                                                   B, nullptr, 0, s));
-            KVHP_TRY(kvhp_rmsnorm_gemv_swiglu_rows_tiled(L.w_gate_up_t, m.hidden, L.ffn_norm,
-                                                         c.rms_eps, m.act, F, H, B, s));
-            KVHP_TRY(kvhp_gemv_residual_rows_tiled(L.w_down_t, m.act, m.hidden, m.hidden, H, F,
-                                                   B, part_need ? m.part_rows : nullptr,
-                                                   part_need, s));
+            KVHP_TRY(residual_rows_act(L.w_o_t, m.attn, m.hidden_t, m.hidden_t, H, Hq * D, B,
+                                       nullptr, 0, 0, nt, hs));
+            KVHP_TRY(swiglu_rows_act(L.w_gate_up_t, m.hidden_t, L.ffn_norm, c.rms_eps, m.act_t,
+                                     F, H, B, nt, hs));
+            KVHP_TRY(residual_rows_act(L.w_down_t, m.act_t, m.hidden_t, m.hidden_t, H, F, B,
+                                       part_need ? m.part_rows : nullptr, part_need, nt, nt, hs));
         }
-        KVHP_TRY(kvhp_rmsnorm_gemv_rows_tiled(m.lm_head_t, m.hidden, m.final_norm, c.rms_eps,
-                                              nullptr, logits, c.vocab_size, H, B, s));
+        KVHP_TRY(rmsnorm_rows_act(m.lm_head_t, m.hidden_t, m.final_norm, c.rms_eps, nullptr,
+                                  logits, c.vocab_size, H, B, nt, hs));
         return kvhp_argmax_rows(logits, B, c.vocab_size, next, s);
     }
     for (int l = 0; l < c.num_layers; ++l) {

@@ -409,6 +409,9 @@ struct RowsArgs {
     int tiles;             // weight tiles
     int live;              // distinct weight rows per tile: 16, or 8 when tiles are
                            // scarce (lanes past it repeat rows; their outputs are dropped)
+    // (on the first 64-byte line of the arguments, with W, x and the sizes)
+    int x_tiles;           // > 0: x row-tiled (act_tiled_index, this many batch tiles)
+    int y_tiles;           // > 0: y16 and resid row-tiled (residual / SwiGLU epilogues)
     f16* y16;              // [B][ldy] (QKV: q [B][Hq*D])
     float* y32;            // [B][ldy]
     const f16* resid;      // [B][ldy], may alias y16
@@ -497,13 +500,22 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
     };
     auto load_x = [&](int bt, half8 (&xs)[C]) {
         const int b = 16 * bt + col;   // columns past B: zero, not loaded
-        if (b < a.B) {
+        if (a.x_tiles) {   // row-tiled: k step (slice, t) of batch tile bt, 1 KB per wave
+#pragma unroll
+            for (int t = 0; t < C; ++t)
+                xs[t] = load_half8(a.x + ((((int64_t)sl * C + t) * a.x_tiles + bt) * kWave + lane) * 8);
+        } else if (b < a.B) {
 #pragma unroll
             for (int t = 0; t < C; ++t) xs[t] = load_half8(a.x + (int64_t)b * a.K + ks + 32 * t);
         } else {
 #pragma unroll
             for (int t = 0; t < C; ++t) xs[t] = half8{};
         }
+    };
+
+    // fp16 output / residual element (b, n): row-major with pitch ldy, or row-tiled
+    auto yat = [&](int b, int n) -> int64_t {
+        return a.y_tiles ? act_tiled_index(b, n, a.y_tiles) : (int64_t)b * a.ldy + n;
     };
 
     half8 wa[C], wb[C];
@@ -519,7 +531,7 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
         // (64j + i) / kCH; rows past B load nothing (zero)
         constexpr int kNL = kStage ? NBT * 16 * kCH / kWave : 1;
         half8 stg[kNL];
-        if constexpr (kStage) {
+        if (kStage && a.x_tiles == 0) {
             const f16* xs0 = a.x + sl * 32 * C;
 #pragma unroll
             for (int j = 0; j < kNL; ++j) {
@@ -527,6 +539,7 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
                 stg[j] = row < a.B ? load_half8(xs0 + (int64_t)row * a.K + 8 * ch) : half8{};
             }
         } else {
+            // row-tiled x (any C), or row-major x outside the staged shapes
 #pragma unroll
             for (int bt = 0; bt < NBT; ++bt) load_x(bt, xr[bt]);
         }
@@ -541,7 +554,7 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
         // every load above in flight before the first use (one round trip;
         // the scheduler would otherwise pair loads with their uses)
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (kStage) {
+        if (kStage && a.x_tiles == 0) {
             // into this wave's region (chunk c of row r at c ^ (r & 7): the
             // 8-lane phases of both the writes and the operand reads hit
             // distinct banks), then back in the layout of the B operand
@@ -652,18 +665,16 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
             dst[d + half] = static_cast<f16>(o2);
         } else if constexpr (EPI == kEpiSwiglu) {
             const int nn = P * tl + m;
-            if (nn < a.N)
-                a.y16[(int64_t)b * a.ldy + nn] = static_cast<f16>(silu_mul(round16(v0), round16(v1)));
+            if (nn < a.N) a.y16[yat(b, nn)] = static_cast<f16>(silu_mul(round16(v0), round16(v1)));
         } else {
             const int nn = L * tl + m;
             if (nn >= a.N) return;
-            const int64_t yo = (int64_t)b * a.ldy + nn;
             if constexpr (EPI == kEpiF32)
-                a.y32[yo] = v0;
+                a.y32[(int64_t)b * a.ldy + nn] = v0;
             else if constexpr (EPI == kEpiResidual)
-                a.y16[yo] = static_cast<f16>(v0 + rv);
+                a.y16[yat(b, nn)] = static_cast<f16>(v0 + rv);
             else
-                a.y16[yo] = static_cast<f16>(v0);
+                a.y16[yat(b, nn)] = static_cast<f16>(v0);
         }
     };
 
@@ -673,7 +684,7 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
         f16 r0 = static_cast<f16>(0.f);
         if constexpr (EPI == kEpiResidual) {
             const int nn = min(L * tl + min((o0 % kOut) / 16, L - 1), a.N - 1);
-            if (o0 < NBT * kOut && b0 < a.B) r0 = a.resid[(int64_t)b0 * a.ldy + nn];
+            if (o0 < NBT * kOut && b0 < a.B) r0 = a.resid[yat(b0, nn)];
         }
         if (pf && kDB) load_w(tl + G, nxt);
         if constexpr (!kDB) load_w(tl, cur);
@@ -722,8 +733,7 @@ __global__ void __launch_bounds__(kWave * NWMAX) gemm_rows_kernel(const RowsArgs
                 if (b < a.B) {
                     if constexpr (EPI == kEpiResidual)
                         rv = static_cast<float>(
-                            a.resid[(int64_t)b * a.ldy +
-                                    min(L * tl + min((o % kOut) / 16, L - 1), a.N - 1)]);
+                            a.resid[yat(b, min(L * tl + min((o % kOut) / 16, L - 1), a.N - 1))]);
                     if constexpr (EPI == kEpiQKV) {
                         pos = a.positions[b];
                         if (pos >= 0 && (pos >> 4) < a.max_pages)
@@ -861,22 +871,34 @@ __global__ void __launch_bounds__(kWave * kWpg) ksplit_partial_kernel(const Rows
 #pragma unroll
         for (int t = 0; t < C; ++t) wr[t] = load_half8_stream(wp + 32 * t);
     }
-    // x slice of every batch row, zero past B
-    for (int i = static_cast<int>(threadIdx.x); i < NBT * 16 * 4 * C; i += kWave * kWpg) {
-        const int r = i / (4 * C), ch = i % (4 * C);   // ch = 4t + k group
-        half8 v = {};
-        if (r < a.B) v = load_half8(a.x + (int64_t)r * a.K + k0 + 8 * ch);
-        xs[r / 16][r % 16][ch / 4][ch % 4] = v;
+    // x slice of every batch row, zero past B; row-tiled x: the slice is one
+    // contiguous run of C * NBT 1 KB blocks, copied as is ([t][bt][lane])
+    half8* xsf = &xs[0][0][0][0];
+    if (a.x_tiles) {
+        const f16* src = a.x + (int64_t)slice * C * NBT * kWave * 8;
+        for (int i = static_cast<int>(threadIdx.x); i < NBT * C * kWave; i += kWave * kWpg)
+            xsf[i] = load_half8(src + (int64_t)i * 8);
+    } else {
+        for (int i = static_cast<int>(threadIdx.x); i < NBT * 16 * 4 * C; i += kWave * kWpg) {
+            const int r = i / (4 * C), ch = i % (4 * C);   // ch = 4t + k group
+            half8 v = {};
+            if (r < a.B) v = load_half8(a.x + (int64_t)r * a.K + k0 + 8 * ch);
+            xs[r / 16][r % 16][ch / 4][ch % 4] = v;
+        }
     }
     __syncthreads();
+    // this lane's operand of (batch tile bt, k step t) at xsf[xo + bt * xsb + t * xst]
+    const int xo = a.x_tiles ? lane : col * C * 4 + g;
+    const int xsb = a.x_tiles ? kWave : 16 * C * 4;
+    const int xst = a.x_tiles ? kWave * NBT : 4;
     floatx4 acc[NBT];
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) {
         acc[bt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < C; ++t)
-            acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wr[t], xs[bt][col][t][g], acc[bt], 0,
-                                                             0, 0);
+            acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wr[t], xsf[xo + bt * xsb + t * xst],
+                                                             acc[bt], 0, 0, 0);
     }
     // lane (g, col): rows 4g..4g+3 of the tile for batch row col of each batch tile
     const int n0 = tile * 16 + 4 * g;
@@ -908,11 +930,11 @@ __global__ void __launch_bounds__(128) ksplit_reduce_residual_kernel(const RowsA
     for (int s = 0; s < kMaxSlices; ++s)
         if (s < slices) v += p[s];
     const int64_t b = o / a.N, n = o % a.N;   // N % 16 == 0: the 4 outputs share a row
+    // (and, row-tiled, one aligned group of 8: contiguous too)
+    const int64_t y0 = a.y_tiles ? act_tiled_index(b, n, a.y_tiles) : b * a.ldy + n;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int64_t yo = b * a.ldy + n + e;
-        a.y16[yo] = static_cast<f16>(v[e] + static_cast<float>(a.resid[yo]));
-    }
+    for (int e = 0; e < 4; ++e)
+        a.y16[y0 + e] = static_cast<f16>(v[e] + static_cast<float>(a.resid[y0 + e]));
 }
 
 // Bytes of fp32 partials the K-split path needs for this call, 0 when the
@@ -1092,6 +1114,17 @@ __global__ void embedding_kernel(const int32_t* ids, const f16* table, f16* out,
     const int64_t id = ids[i];
     for (int64_t k = threadIdx.x; k < hidden; k += blockDim.x)
         out[i * hidden + k] = (id >= 0 && id < vocab) ? table[id * hidden + k] : static_cast<f16>(0.f);
+}
+
+// The same rows into row-tiled activations (hidden % 32 == 0, 16-byte
+// aligned table): 8 columns per thread, contiguous in both layouts.
+__global__ void embedding_tiled_kernel(const int32_t* ids, const f16* table, f16* out,
+                                       int64_t hidden, int64_t vocab, int nbt) {
+    const int64_t i = blockIdx.x;
+    const int64_t id = ids[i];
+    const bool ok = id >= 0 && id < vocab;
+    for (int64_t k = 8 * threadIdx.x; k < hidden; k += 8 * blockDim.x)
+        store_half8(out + act_tiled_index(i, k, nbt), ok ? load_half8(table + id * hidden + k) : half8{});
 }
 
 // Greedy argmax of fp32 logits, lowest index on ties; NaN never wins.
@@ -1352,7 +1385,7 @@ int rmsnorm_qkv_rope_append_at(const void* W_qkv, const void* x, const void* nor
 
 int residual_rows_impl(const void* W, const void* Wt, const void* x, const void* r, void* y,
                        int N, int K, int batch, void* workspace, size_t workspace_bytes,
-                       hipStream_t s, const char* what) {
+                       hipStream_t s, const char* what, int x_tiles = 0, int y_tiles = 0) {
     if (N == 0 || batch == 0) return KVHP_OK;
     int rc = check_gemv(W ? W : Wt, x, N, K, what);
     if (rc) return rc;
@@ -1367,6 +1400,8 @@ int residual_rows_impl(const void* W, const void* Wt, const void* x, const void*
     a.resid = static_cast<const f16*>(r);
     a.y16 = static_cast<f16*>(y);
     a.ldy = N;
+    a.x_tiles = x_tiles;
+    a.y_tiles = y_tiles;
     const size_t need = ksplit_bytes(N, K, batch);
     if (need == 0 || workspace == nullptr) return launch_rows<kEpiResidual, false>(a, s, what);
     KVHP_REQUIRE(workspace_bytes >= need, KVHP_ERR_WORKSPACE,
@@ -1407,7 +1442,7 @@ extern "C" int kvhp_gemv_residual_rows_tiled(const void* W_tiled, const void* x,
 
 int rmsnorm_rows_impl(const void* W, const void* Wt, const void* x, const void* norm_w,
                       float eps, void* y16, float* y32, int N, int K, int batch, hipStream_t s,
-                      const char* what) {
+                      const char* what, int act_tiles = 0) {
     if (N == 0 || batch == 0) return KVHP_OK;
     int rc = check_gemv(W ? W : Wt, x, N, K, what);
     if (rc) return rc;
@@ -1426,6 +1461,8 @@ int rmsnorm_rows_impl(const void* W, const void* Wt, const void* x, const void* 
     a.y16 = static_cast<f16*>(y16);
     a.y32 = y32;
     a.ldy = N;
+    a.x_tiles = act_tiles;
+    a.y_tiles = y16 ? act_tiles : 0;
     return y32 ? launch_rows<kEpiF32, true>(a, s, what) : launch_rows<kEpiF16, true>(a, s, what);
 }
 
@@ -1447,7 +1484,8 @@ extern "C" int kvhp_rmsnorm_gemv_rows_tiled(const void* W_tiled, const void* x,
 }
 
 int swiglu_rows_impl(const void* W, const void* Wt, const void* x, const void* norm_w, float eps,
-                     void* out, int N, int K, int batch, hipStream_t s, const char* what) {
+                     void* out, int N, int K, int batch, hipStream_t s, const char* what,
+                     int act_tiles = 0) {
     if (N == 0 || batch == 0) return KVHP_OK;
     int rc = check_gemv(W ? W : Wt, x, N, K, what);
     if (rc) return rc;
@@ -1463,6 +1501,8 @@ int swiglu_rows_impl(const void* W, const void* Wt, const void* x, const void* n
     a.B = batch;
     a.y16 = static_cast<f16*>(out);
     a.ldy = N;
+    a.x_tiles = act_tiles;
+    a.y_tiles = act_tiles;
     return launch_rows<kEpiSwiglu, true>(a, s, what);
 }
 
@@ -1487,7 +1527,7 @@ int qkv_rows_impl(const void* W_qkv, const void* Wt, const void* x, const void* 
                   const int32_t* positions, float rope_theta, void* q_out, void* pool_k,
                   void* pool_v, const int32_t* block_tables, int max_pages, int num_pages,
                   int num_q_heads, int num_kv_heads, int head_dim, int K, int batch,
-                  hipStream_t s, const char* what) {
+                  hipStream_t s, const char* what, int act_tiles = 0) {
     if (batch == 0) return KVHP_OK;
     const int N = (num_q_heads + 2 * num_kv_heads) * head_dim;
     int rc = check_gemv(W_qkv ? W_qkv : Wt, x, N, K, what);
@@ -1518,6 +1558,7 @@ int qkv_rows_impl(const void* W_qkv, const void* Wt, const void* x, const void* 
     a.bt = block_tables;
     a.max_pages = max_pages;
     a.num_pages = num_pages;
+    a.x_tiles = act_tiles;
     return launch_rows<kEpiQKV, true>(a, s, what);
 }
 
@@ -1545,6 +1586,67 @@ extern "C" int kvhp_rmsnorm_qkv_rope_append_rows_tiled(
                          head_dim, K, batch, static_cast<hipStream_t>(stream),
                          "rmsnorm_qkv_rope_append_rows_tiled");
 }
+
+namespace kvhp {
+namespace {
+// Row-tiled activations need the batch's tile count and whole 32-column
+// steps on both sides.
+int check_act(int act_tiles, int batch, int K, int N, const char* what) {
+    KVHP_REQUIRE(act_tiles == 0 || (act_tiles == act_tiles_for(batch) && K % 32 == 0 &&
+                                    N % 32 == 0),
+                 KVHP_ERR_INVALID, "%s: %d activation tiles for batch %d, K=%d N=%d", what,
+                 act_tiles, batch, K, N);
+    return KVHP_OK;
+}
+}  // namespace
+
+int residual_rows_act(const void* Wt, const void* x, const void* r, void* y, int N, int K,
+                      int batch, void* workspace, size_t workspace_bytes, int x_tiles,
+                      int y_tiles, hipStream_t s) {
+    if (int rc = check_act(x_tiles, batch, K, 32, "residual_rows_act")) return rc;
+    if (int rc = check_act(y_tiles, batch, 32, N, "residual_rows_act")) return rc;
+    return residual_rows_impl(nullptr, Wt, x, r, y, N, K, batch, workspace, workspace_bytes, s,
+                              "residual_rows_act", x_tiles, y_tiles);
+}
+
+int rmsnorm_rows_act(const void* Wt, const void* x, const void* norm_w, float eps, void* y16,
+                     float* y32, int N, int K, int batch, int act_tiles, hipStream_t s) {
+    if (int rc = check_act(act_tiles, batch, K, y16 ? N : 32, "rmsnorm_rows_act")) return rc;
+    return rmsnorm_rows_impl(nullptr, Wt, x, norm_w, eps, y16, y32, N, K, batch, s,
+                             "rmsnorm_rows_act", act_tiles);
+}
+
+int swiglu_rows_act(const void* Wt, const void* x, const void* norm_w, float eps, void* out,
+                    int N, int K, int batch, int act_tiles, hipStream_t s) {
+    if (int rc = check_act(act_tiles, batch, K, N, "swiglu_rows_act")) return rc;
+    return swiglu_rows_impl(nullptr, Wt, x, norm_w, eps, out, N, K, batch, s, "swiglu_rows_act",
+                            act_tiles);
+}
+
+int qkv_rows_act(const void* Wt, const void* x, const void* norm_w, float eps,
+                 const int32_t* positions, float rope_theta, void* q_out, void* pool_k,
+                 void* pool_v, const int32_t* block_tables, int max_pages, int num_pages,
+                 int num_q_heads, int num_kv_heads, int head_dim, int K, int batch, int act_tiles,
+                 hipStream_t s) {
+    if (int rc = check_act(act_tiles, batch, K, 32, "qkv_rows_act")) return rc;
+    return qkv_rows_impl(nullptr, Wt, x, norm_w, eps, positions, rope_theta, q_out, pool_k,
+                         pool_v, block_tables, max_pages, num_pages, num_q_heads, num_kv_heads,
+                         head_dim, K, batch, s, "qkv_rows_act", act_tiles);
+}
+
+int embedding_act(const int32_t* token_ids, const void* table, void* out, int batch,
+                  int64_t hidden, int64_t vocab, int act_tiles, hipStream_t s) {
+    if (act_tiles == 0) return kvhp_embedding(token_ids, table, out, batch, hidden, vocab, s);
+    if (batch <= 0) return KVHP_OK;
+    KVHP_REQUIRE(token_ids && table && out && vocab > 0 && hidden > 0 && hidden % 32 == 0 &&
+                     act_tiles == act_tiles_for(batch) && aligned16(table) && aligned16(out),
+                 KVHP_ERR_INVALID, "embedding_act: bad arguments");
+    hipLaunchKernelGGL(embedding_tiled_kernel, dim3(static_cast<unsigned>(batch)), dim3(256), 0, s,
+                       token_ids, static_cast<const f16*>(table), static_cast<f16*>(out), hidden,
+                       vocab, act_tiles);
+    return check_launch("embedding_act");
+}
+}  // namespace kvhp
 
 extern "C" size_t kvhp_rows_tiled_bytes(int kind, int N, int K, int num_q_heads,
                                         int num_kv_heads, int head_dim) {

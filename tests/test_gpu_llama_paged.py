@@ -411,6 +411,84 @@ def test_decode_paged_graph_capture_needs_reserve():
     model.close()
 
 
+@pytest.mark.parametrize("B", [3, 17])
+def test_batched_step_is_the_exported_operators(B):
+    """The runner's batched step keeps its hidden state and SwiGLU output
+    row-tiled between launches; the exported operators take row-major
+    activations.  One step of B sequences through kvhp_llama_decode_paged
+    against the same step composed from the exported calls (embedding,
+    kvhp_rmsnorm_qkv_rope_append_rows_tiled, kvhp_decode_attention,
+    kvhp_gemv_residual_rows_tiled for o and down, the SwiGLU and LM-head
+    projections) on weights tiled with kvhp_rows_tile_weights: logits, greedy
+    tokens and the appended K/V bit for bit.  FFN 5632: B = 17 splits the
+    down projection over K, B = 3 does not; B = 17 also has two batch tiles
+    with 15 padding rows."""
+    cfg = _cfg(5632)
+    L, Hq, Hkv, D, V = (cfg.num_layers, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
+                        cfg.vocab_size)
+    H, F, eps, theta = cfg.hidden_size, cfg.ffn_size, cfg.rms_eps, cfg.rope_theta
+    plen, max_pages = 13, 2
+    P = B * max_pages
+    rng = np.random.default_rng(777 + B)
+    model = kvhp.LlamaModel(cfg, seed=31, max_ctx=64)
+    pool = torch.zeros(L * 2 * Hkv * P * PAGE * D, dtype=torch.float16, device="cuda")
+    bt = torch.from_numpy(rng.permutation(P).astype(np.int32).reshape(B, max_pages)).cuda()
+    toks = torch.tensor([model.prefill_paged(rng.integers(0, V, plen).astype(np.int32), pool, P,
+                                             bt[b], max_pages)[0] for b in range(B)],
+                        dtype=torch.int32, device="cuda")
+    pos = torch.full((B,), plen, dtype=torch.int32, device="cuda")
+    sl = pos + 1
+    max_len = plen + 1
+
+    pool_r = pool.clone()
+    lg_r = torch.empty(B, V, dtype=torch.float32, device="cuda")
+    nx_r = torch.empty(B, dtype=torch.int32, device="cuda")
+    model.decode_paged(toks, pool_r, P, bt, max_pages, pos, sl, max_len, lg_r, nx_r)
+
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+    def tiled(kind, W, N, K):
+        out = torch.empty(kvhp.rows_tiled_bytes(kind, N, K, Hq, Hkv, D) // 2,
+                          dtype=torch.float16, device="cuda")
+        kvhp.rows_tile_weights(kind, dev(W), N, K, out, Hq, Hkv, D)
+        return out
+
+    pool_e = pool.clone()
+    pools = pool_e.view(L, 2, Hkv, P, PAGE, D)
+    x = torch.empty(B, H, dtype=torch.float16, device="cuda")
+    kvhp.embedding(toks, dev(model.tensor(-1, kvhp.LLAMA_EMBED)), x, B, H, V)
+    q = torch.empty(B, Hq * D, dtype=torch.float16, device="cuda")
+    attn = torch.empty(B, Hq * D, dtype=torch.float16, device="cuda")
+    act = torch.empty(B, F, dtype=torch.float16, device="cuda")
+    ws = torch.empty(max(kvhp.decode_workspace_bytes(B, Hq, Hkv, D, max_len), 16),
+                     dtype=torch.uint8, device="cuda")
+    part = torch.empty(max(kvhp.gemv_rows_workspace_bytes(H, F, B), 16), dtype=torch.uint8,
+                       device="cuda")
+    assert (kvhp.gemv_rows_workspace_bytes(H, F, B) > 0) == (B == 17)
+    for li in range(L):
+        w = lambda which: model.tensor(li, which)
+        kvhp.rmsnorm_qkv_rope_append_rows_tiled(
+            tiled(kvhp.ROWS_QKV, w(kvhp.LLAMA_W_QKV), 0, H), x, dev(w(kvhp.LLAMA_ATTN_NORM)), eps,
+            pos, theta, q, pools[li, 0], pools[li, 1], bt, Hq, Hkv, D, H, B)
+        kvhp.decode_attention(q, kvhp.paged_view(pools[li, 0], bt), kvhp.paged_view(pools[li, 1], bt),
+                              sl, attn, Hq, Hkv, D, max_len, 0, ws)
+        kvhp.gemv_residual_rows_tiled(tiled(kvhp.ROWS_PLAIN, w(kvhp.LLAMA_W_O), H, Hq * D), attn,
+                                      x, x, H, Hq * D, B)
+        kvhp.rmsnorm_gemv_swiglu_rows_tiled(tiled(kvhp.ROWS_SWIGLU, w(kvhp.LLAMA_W_GATE_UP), F, H),
+                                            x, dev(w(kvhp.LLAMA_FFN_NORM)), eps, act, F, H, B)
+        kvhp.gemv_residual_rows_tiled(tiled(kvhp.ROWS_PLAIN, w(kvhp.LLAMA_W_DOWN), H, F), act, x, x,
+                                      H, F, B, workspace=part)
+    lg_e = torch.empty(B, V, dtype=torch.float32, device="cuda")
+    kvhp.rmsnorm_gemv_rows_tiled(tiled(kvhp.ROWS_PLAIN, model.tensor(-1, kvhp.LLAMA_LM_HEAD), V, H),
+                                 x, dev(model.tensor(-1, kvhp.LLAMA_FINAL_NORM)), eps, V, H, B,
+                                 y32=lg_e)
+    torch.cuda.synchronize()
+    assert torch.equal(lg_r, lg_e), "runner logits differ from the exported operators'"
+    assert torch.equal(nx_r.long(), lg_e.argmax(dim=1)), "greedy tokens"
+    assert torch.equal(pool_r, pool_e), "appended K/V differ"
+    model.close()
+
+
 def test_batched_steps_see_rewritten_weights_after_reserve():
     """Batched steps (2..32 rows) read the model's tiled copies of the four
     projections and the LM head, built on the first batched step.  Weights
