@@ -91,6 +91,11 @@ struct DecodeArgs {
     int cap;               // tokens addressable per sequence
     int fixed_len;         // length of every sequence when seq_lens == nullptr
     float scale_log2;      // log2(e) / sqrt(D)
+    // > 0: out is row-tiled ([B][Hq*D] in act_tiled_index order, this many
+    // batch tiles; the batched model runner's o-projection input), written by
+    // the kernels instantiated for it; 0: row-major.  (In the padding before
+    // k_new: no other argument moves.)
+    int out_tiles;
     // Fused append (k_new == nullptr: none): row b of k_new / v_new
     // [B][Hkv][D] is the token at position new_pos[b]; the split that covers
     // it writes it into its page (or its row of a strided view) before
@@ -169,7 +174,7 @@ __device__ __forceinline__ half8 cat_half8(short4v lo, short4v hi) {
 // K runs two of the wave's steps ahead in registers, V one; both are loaded as whole
 // rows and staged through LDS (K for the A layout, V for the transposed
 // reads).
-template <int D, int G, bool PAGED, int W>
+template <int D, int G, bool PAGED, int W, bool TOUT = false>
 __global__ void __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_splitk_kernel(const DecodeArgs a) {
     static_assert(G >= 1 && G <= 16, "one MFMA column per query head");
@@ -314,7 +319,11 @@ decode_splitk_kernel(const DecodeArgs a) {
         if (split == 0) {
             const half8 z = {};
             for (int i = lane; i < G * LPR; i += kWave)
-                store_half8(a.out + (row0 + i / LPR) * D + 8 * (i % LPR), z);
+                if constexpr (TOUT)
+                    store_half8(a.out + act_tiled_index(b, (int64_t)(kvh * G + i / LPR) * D +
+                                                               8 * (i % LPR), a.out_tiles), z);
+                else
+                    store_half8(a.out + (row0 + i / LPR) * D + 8 * (i % LPR), z);
         }
         return;
     }
@@ -561,7 +570,12 @@ decode_splitk_kernel(const DecodeArgs a) {
             half4 h;
 #pragma unroll
             for (int e = 0; e < 4; ++e) h[e] = static_cast<f16>(o[db][e] * inv);
-            *reinterpret_cast<half4*>(orow + 16 * db) = h;
+            if constexpr (TOUT)
+                *reinterpret_cast<half4*>(
+                    a.out + act_tiled_index(b, (int64_t)(kvh * G + col) * D + 4 * g + 16 * db,
+                                            a.out_tiles)) = h;
+            else
+                *reinterpret_cast<half4*>(orow + 16 * db) = h;
         }
         return;
     }
@@ -583,7 +597,7 @@ decode_splitk_kernel(const DecodeArgs a) {
 // relative to the split's own max m (log2 units).
 constexpr int kMergeWaves = 4;
 
-template <int D, int G>
+template <int D, int G, bool TOUT = false>
 __global__ void __launch_bounds__(kMergeWaves * kWave)
 decode_merge_kernel(const DecodeArgs a) {
     constexpr int LPR = D / 8;          // lanes per head row (8 dims each)
@@ -675,7 +689,11 @@ decode_merge_kernel(const DecodeArgs a) {
             hv[e] = static_cast<f16>(acc[p][0][e] * inv);
             hv[4 + e] = static_cast<f16>(acc[p][1][e] * inv);
         }
-        store_half8(a.out + (row0 + h) * D + 8 * (lane % LPR), hv);
+        if constexpr (TOUT)
+            store_half8(a.out + act_tiled_index(b, (int64_t)(kvh * G + h) * D + 8 * (lane % LPR),
+                                                a.out_tiles), hv);
+        else
+            store_half8(a.out + (row0 + h) * D + 8 * (lane % LPR), hv);
     }
 }
 
@@ -688,7 +706,7 @@ decode_merge_kernel(const DecodeArgs a) {
 // trip); slots past the sequence's last split are dropped by selects (their
 // contents may be stale).  The subsets fold by lane exchanges, the waves
 // through LDS.
-template <int D>
+template <int D, bool TOUT = false>
 __global__ void __launch_bounds__(kMergeWaves * kWave)
 decode_merge_rows_kernel(const DecodeArgs a) {
     constexpr int LPR = D / 8;
@@ -788,7 +806,10 @@ decode_merge_rows_kernel(const DecodeArgs a) {
         hv[e] = static_cast<f16>(acc0[e] * inv);
         hv[4 + e] = static_cast<f16>(acc1[e] * inv);
     }
-    store_half8(a.out + row * D + 8 * c, hv);
+    if constexpr (TOUT)
+        store_half8(a.out + act_tiled_index(b, (int64_t)blockIdx.x * D + 8 * c, a.out_tiles), hv);
+    else
+        store_half8(a.out + row * D + 8 * c, hv);
 }
 
 // Append of one token per sequence into strided views (the fused append's
@@ -823,9 +844,13 @@ decode_generic_kernel(const DecodeArgs a, int D, int G) {
     const int64_t row = (int64_t)b * a.Hq + qh;
     int L = seq_len_of(a, b);
     if (L > a.cap) L = a.cap;
-    f16* o = a.out + row * D;
+    // the fallback honours a row-tiled output at run time
+    auto o_at = [&](int d) -> f16* {
+        return a.out_tiles ? a.out + act_tiled_index(b, (int64_t)qh * D + d, a.out_tiles)
+                           : a.out + row * D + d;
+    };
     if (L <= 0) {
-        for (int d = lane; d < D; d += kWave) o[d] = f16(0);
+        for (int d = lane; d < D; d += kWave) *o_at(d) = f16(0);
         return;
     }
     float qv[4], acc[4];
@@ -875,7 +900,7 @@ decode_generic_kernel(const DecodeArgs a, int D, int G) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int d = lane + kWave * i;
-        if (d < D) o[d] = static_cast<f16>(acc[i] * inv);
+        if (d < D) *o_at(d) = static_cast<f16>(acc[i] * inv);
     }
 }
 
@@ -1031,14 +1056,14 @@ int resident_splits(K kernel) {
     return resident_workgroups(reinterpret_cast<const void*>(kernel), kWave);
 }
 
-template <int D, int G>
+template <int D, int G, bool TOUT>
 void launch_fast(const DecodeArgs& args, dim3 grid, bool paged, hipStream_t s) {
     DecodeArgs a = args;
     if (a.balance > 0) {
         // Balanced splits: about one split per resident wave slot over the
         // batch, less half a split per sequence for the rounding up of each
         // sequence's split count.
-        const int slots = paged ? resident_splits(decode_splitk_kernel<D, G, true, 1>)
+        const int slots = paged ? resident_splits(decode_splitk_kernel<D, G, true, 1, TOUT>)
                                 : resident_splits(decode_splitk_kernel<D, G, false, 1>);
         a.balance = slots > 0 ? max(1, slots / a.Hkv - a.batch / 2) : 0;
         if (a.balance > 0) {
@@ -1056,17 +1081,17 @@ void launch_fast(const DecodeArgs& args, dim3 grid, bool paged, hipStream_t s) {
     }
     if (a.balance > 0) {   // the work list: one wave per split
         if (paged)
-            hipLaunchKernelGGL((decode_splitk_kernel<D, G, true, 1>), grid, dim3(kWave), 0, s, a);
+            hipLaunchKernelGGL((decode_splitk_kernel<D, G, true, 1, TOUT>), grid, dim3(kWave), 0, s, a);
         else
             hipLaunchKernelGGL((decode_splitk_kernel<D, G, false, 1>), grid, dim3(kWave), 0, s, a);
     } else if (D == 64 || a.nsplit == 1) {   // fixed chunks: four waves per split
         if (paged)
-            hipLaunchKernelGGL((decode_splitk_kernel<D, G, true, 4>), grid, dim3(4 * kWave), 0, s, a);
+            hipLaunchKernelGGL((decode_splitk_kernel<D, G, true, 4, TOUT>), grid, dim3(4 * kWave), 0, s, a);
         else
             hipLaunchKernelGGL((decode_splitk_kernel<D, G, false, 4>), grid, dim3(4 * kWave), 0, s, a);
     } else {
         if (paged)
-            hipLaunchKernelGGL((decode_splitk_kernel<D, G, true, 1>), grid, dim3(kWave), 0, s, a);
+            hipLaunchKernelGGL((decode_splitk_kernel<D, G, true, 1, TOUT>), grid, dim3(kWave), 0, s, a);
         else
             hipLaunchKernelGGL((decode_splitk_kernel<D, G, false, 1>), grid, dim3(kWave), 0, s, a);
     }
@@ -1076,25 +1101,34 @@ void launch_fast(const DecodeArgs& args, dim3 grid, bool paged, hipStream_t s) {
     const bool rows_merge =
         a.balance <= 0 && (long long)a.nsplit * G * (D + 2) * sizeof(float) >= (64 << 10);
     if (a.nsplit > 1 && rows_merge)
-        hipLaunchKernelGGL((decode_merge_rows_kernel<D>), dim3(a.Hq, a.batch),
+        hipLaunchKernelGGL((decode_merge_rows_kernel<D, TOUT>), dim3(a.Hq, a.batch),
                            dim3(kMergeWaves * kWave), 0, s, a);
     else if (a.nsplit > 1)
-        hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(a.Hkv, a.batch),
+        hipLaunchKernelGGL((decode_merge_kernel<D, G, TOUT>), dim3(a.Hkv, a.batch),
                            dim3(kMergeWaves * kWave), 0, s, a);
+}
+
+// A row-tiled output on paged views only (the model runner's pools).
+template <int D, int G>
+void launch_out(const DecodeArgs& a, dim3 grid, bool paged, hipStream_t s) {
+    if (a.out_tiles > 0 && paged)
+        launch_fast<D, G, true>(a, grid, paged, s);
+    else
+        launch_fast<D, G, false>(a, grid, paged, s);
 }
 
 template <int D>
 bool dispatch_g(int G, const DecodeArgs& a, dim3 grid, bool paged, hipStream_t s) {
     switch (G) {
-        case 1: launch_fast<D, 1>(a, grid, paged, s); return true;
-        case 2: launch_fast<D, 2>(a, grid, paged, s); return true;
-        case 3: launch_fast<D, 3>(a, grid, paged, s); return true;
-        case 4: launch_fast<D, 4>(a, grid, paged, s); return true;
-        case 5: launch_fast<D, 5>(a, grid, paged, s); return true;
-        case 6: launch_fast<D, 6>(a, grid, paged, s); return true;
-        case 7: launch_fast<D, 7>(a, grid, paged, s); return true;
-        case 8: launch_fast<D, 8>(a, grid, paged, s); return true;
-        case 16: launch_fast<D, 16>(a, grid, paged, s); return true;
+        case 1: launch_out<D, 1>(a, grid, paged, s); return true;
+        case 2: launch_out<D, 2>(a, grid, paged, s); return true;
+        case 3: launch_out<D, 3>(a, grid, paged, s); return true;
+        case 4: launch_out<D, 4>(a, grid, paged, s); return true;
+        case 5: launch_out<D, 5>(a, grid, paged, s); return true;
+        case 6: launch_out<D, 6>(a, grid, paged, s); return true;
+        case 7: launch_out<D, 7>(a, grid, paged, s); return true;
+        case 8: launch_out<D, 8>(a, grid, paged, s); return true;
+        case 16: launch_out<D, 16>(a, grid, paged, s); return true;
         default: return false;
     }
 }
@@ -1122,7 +1156,7 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
                           int hq, int hkv, int d, int max_seq_len, int num_splits,
                           void* workspace, size_t workspace_bytes, hipStream_t s,
                           const void* k_new = nullptr, const void* v_new = nullptr,
-                          const int32_t* new_pos = nullptr) {
+                          const int32_t* new_pos = nullptr, int out_tiles = 0) {
     if (batch <= 0 || max_seq_len <= 0) return KVHP_OK;
     KVHP_REQUIRE(q && out, KVHP_ERR_INVALID, "decode_attention: null pointer");
     KVHP_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0, KVHP_ERR_INVALID,
@@ -1154,6 +1188,7 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
     a.new_pos = nullptr;
     a.pool_k = const_cast<f16*>(static_cast<const f16*>(kv->data));
     a.pool_v = const_cast<f16*>(static_cast<const f16*>(vv->data));
+    a.out_tiles = out_tiles;
 
     // The fast kernel reads one block table for K and V (one page id per
     // token position, the layout PagedKVCache builds).
@@ -1254,6 +1289,21 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
                             : dispatch_g<128>(G, a, grid, paged, s);
     if (!ok) return fail(KVHP_ERR_UNSUPPORTED, "decode_attention: group size %d", G);
     return check_launch("decode_attention");
+}
+
+int decode_attention_act(const void* q, const kvhp_kv_view* k_view, const kvhp_kv_view* v_view,
+                         const int32_t* seq_lens, void* out, int batch, int num_q_heads,
+                         int num_kv_heads, int head_dim, int max_seq_len, void* workspace,
+                         size_t workspace_bytes, int act_tiles, hipStream_t s) {
+    KVHP_REQUIRE(seq_lens && k_view && k_view->block_table, KVHP_ERR_INVALID,
+                 "decode_attention_act: paged views and seq_lens required");
+    KVHP_REQUIRE(act_tiles == act_tiles_for(batch) && (int64_t)num_q_heads * head_dim % 32 == 0 &&
+                     aligned16(out),
+                 KVHP_ERR_INVALID, "decode_attention_act: %d output tiles for batch %d, Hq*D=%d",
+                 act_tiles, batch, num_q_heads * head_dim);
+    return decode_attention_impl(q, k_view, v_view, seq_lens, 0, out, batch, num_q_heads,
+                                 num_kv_heads, head_dim, max_seq_len, 0, workspace,
+                                 workspace_bytes, s, nullptr, nullptr, nullptr, act_tiles);
 }
 
 }  // namespace kvhp

@@ -51,8 +51,8 @@ int rmsnorm_qkv_rope_append_at(const void* W_qkv, const void* x, const void* nor
                                int max_pages, int num_pages, int num_q_heads, int num_kv_heads,
                                int head_dim, int K, hipStream_t stream);
 
-// Row-tiled activations: the batched runner keeps its hidden state and
-// SwiGLU output ([B][K], K % 32 == 0) in the lane order of the 16x16x32 MFMA
+// Row-tiled activations: the batched runner keeps its hidden state, attention
+// output and SwiGLU output ([B][K], K % 32 == 0) in the lane order of the 16x16x32 MFMA
 // B operand, so that the batched projections load one k step of 16 batch
 // rows as 1 KB contiguous per wave instead of staging row-major rows through
 // LDS.  Element (b, k) sits at act_tiled_index(b, k,
@@ -73,7 +73,7 @@ inline int act_tiles_for(int batch) { return (batch + 15) / 16; }
 // kvhp_rmsnorm_qkv_rope_append_rows_tiled and kvhp_embedding, with x, the
 // residual and fp16 outputs in that layout (q, the pages and fp32 logits stay
 // as they are).  The residual projection takes the layouts of x and of the
-// residual stream separately: the attention output it reads stays row-major.
+// residual stream separately.
 int residual_rows_act(const void* Wt, const void* x, const void* r, void* y, int N, int K,
                       int batch, void* workspace, size_t workspace_bytes, int x_tiles,
                       int y_tiles, hipStream_t s);
@@ -88,6 +88,13 @@ int qkv_rows_act(const void* Wt, const void* x, const void* norm_w, float eps,
                  hipStream_t s);
 int embedding_act(const int32_t* token_ids, const void* table, void* out, int batch,
                   int64_t hidden, int64_t vocab, int act_tiles, hipStream_t s);
+// decode.hip: kvhp_decode_attention on paged views writing its output [B][Hq*D]
+// row-tiled (act_tiles = act_tiles_for(batch)); the fast kernels are
+// instantiated separately for it, so row-major calls run unchanged code.
+int decode_attention_act(const void* q, const kvhp_kv_view* k_view, const kvhp_kv_view* v_view,
+                         const int32_t* seq_lens, void* out, int batch, int num_q_heads,
+                         int num_kv_heads, int head_dim, int max_seq_len, void* workspace,
+                         size_t workspace_bytes, int act_tiles, hipStream_t s);
 
 #define KVHP_REQUIRE(cond, code, ...)          \
     do {                                       \

@@ -98,8 +98,8 @@ struct Model {
     f16* lm_head_t = nullptr;  // LM head tiled for the batched kernels
     bool tiled = false;        // the tiled copies hold the current weights
     // batched-step activations (2..32 rows), row-tiled (act_tiled_index):
-    // hidden [32][H], SwiGLU output [32][F]
-    f16 *hidden_t = nullptr, *act_t = nullptr;
+    // hidden [32][H], attention output [32][Hq*D], SwiGLU output [32][F]
+    f16 *hidden_t = nullptr, *attn_t = nullptr, *act_t = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
 
@@ -403,6 +403,7 @@ int build_tiled(Model& m, hipStream_t s) {
     KVHP_TRY(tile(&m.lm_head_t, KVHP_ROWS_PLAIN, m.lm_head, c.vocab_size, H));
     if (!m.hidden_t) {
         KVHP_TRY(alloc_n(m, (size_t)32 * H, &m.hidden_t));
+        KVHP_TRY(alloc_n(m, (size_t)32 * Hq * D, &m.attn_t));
         KVHP_TRY(alloc_n(m, (size_t)32 * F, &m.act_t));
     }
     m.tiled = true;
@@ -454,11 +455,10 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
         // weight read once per step for all B rows, from its tiled copy, six
         // launches per layer (seven when the down projection's x is large
         // enough to split over K: its partials live in the model's own
-        // buffer).  The hidden state and the SwiGLU output stay row-tiled,
-        // so the projections that read them load x as 1 KB contiguous per
-        // wave and k step (bit-identical to row-major activations: the same
-        // operands); the attention output stays row-major (the o projection
-        // stages it through LDS as before).
+        // buffer).  The activations between them (hidden state, attention
+        // output, SwiGLU output) stay row-tiled, so every projection loads
+        // its x as 1 KB contiguous per wave and k step (bit-identical to
+        // row-major activations: the same operands).
         const int nt = act_tiles_for(B);
         const hipStream_t hs = static_cast<hipStream_t>(s);
         const size_t part_need = kvhp_gemv_rows_workspace_bytes(H, F, B);
@@ -476,10 +476,10 @@ int decode_rows(Model& m, const int32_t* tokens, int B, const Pages& pg,
                                   layer_pool(m, pg, l, 1), wbt, pg.max_pages, pg.num_pages, Hq,
                                   Hkv, D, H, B, nt, hs));
             const kvhp_kv_view kv = pages_view(m, pg, l, 0), vv = pages_view(m, pg, l, 1);
-            KVHP_TRY(kvhp_decode_attention(m.q, &kv, &vv, seq_lens, m.attn, B, Hq, Hkv, D,
-                                           max_seq_len, 0, ws, ws_bytes, s));
-            KVHP_TRY(residual_rows_act(L.w_o_t, m.attn, m.hidden_t, m.hidden_t, H, Hq * D, B,
-                                       nullptr, 0, 0, nt, hs));
+            KVHP_TRY(decode_attention_act(m.q, &kv, &vv, seq_lens, m.attn_t, B, Hq, Hkv, D,
+                                          max_seq_len, ws, ws_bytes, nt, hs));
+            KVHP_TRY(residual_rows_act(L.w_o_t, m.attn_t, m.hidden_t, m.hidden_t, H, Hq * D, B,
+                                       nullptr, 0, nt, nt, hs));
             KVHP_TRY(swiglu_rows_act(L.w_gate_up_t, m.hidden_t, L.ffn_norm, c.rms_eps, m.act_t,
                                      F, H, B, nt, hs));
             KVHP_TRY(residual_rows_act(L.w_down_t, m.act_t, m.hidden_t, m.hidden_t, H, F, B,

@@ -411,26 +411,33 @@ def test_decode_paged_graph_capture_needs_reserve():
     model.close()
 
 
-@pytest.mark.parametrize("B", [3, 17])
-def test_batched_step_is_the_exported_operators(B):
-    """The runner's batched step keeps its hidden state and SwiGLU output
-    row-tiled between launches; the exported operators take row-major
-    activations.  One step of B sequences through kvhp_llama_decode_paged
-    against the same step composed from the exported calls (embedding,
-    kvhp_rmsnorm_qkv_rope_append_rows_tiled, kvhp_decode_attention,
-    kvhp_gemv_residual_rows_tiled for o and down, the SwiGLU and LM-head
-    projections) on weights tiled with kvhp_rows_tile_weights: logits, greedy
-    tokens and the appended K/V bit for bit.  FFN 5632: B = 17 splits the
-    down projection over K, B = 3 does not; B = 17 also has two batch tiles
-    with 15 padding rows."""
-    cfg = _cfg(5632)
+@pytest.mark.parametrize("shape,B,plen", [("d64", 3, 13), ("d64", 17, 13), ("d128", 2, 4190),
+                                          ("d32", 5, 20)])
+def test_batched_step_is_the_exported_operators(shape, B, plen):
+    """The runner's batched step keeps its hidden state, attention output
+    and SwiGLU output row-tiled between launches; the exported operators
+    take row-major activations.  One step of B sequences through
+    kvhp_llama_decode_paged against the same step composed from the
+    exported calls (embedding, kvhp_rmsnorm_qkv_rope_append_rows_tiled,
+    kvhp_decode_attention, kvhp_gemv_residual_rows_tiled for o and down,
+    the SwiGLU and LM-head projections) on weights tiled with
+    kvhp_rows_tile_weights: logits, greedy tokens and the appended K/V bit
+    for bit.  Every attention kernel that writes the tiled output runs:
+    d64 (FFN 5632) B = 3 one split per sequence, written by the split
+    kernel (fixed chunks, four waves per split), B = 17 balanced splits
+    and the per-KV-head merge, with the down projection split over K and
+    15 padding rows; d128 B = 2 at 4191 keys 33 fixed splits and the
+    per-query-head merge; d32 the generic kernel."""
+    cfg = {"d64": _cfg(5632),
+           "d128": kvhp.LlamaConfig(2048, 1024, 2, 8, 2, 128, 1024, 1e-5, 10000.0, 0),
+           "d32": kvhp.LlamaConfig(2048, 256, 2, 8, 2, 32, 512, 1e-5, 10000.0, 0)}[shape]
     L, Hq, Hkv, D, V = (cfg.num_layers, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
                         cfg.vocab_size)
     H, F, eps, theta = cfg.hidden_size, cfg.ffn_size, cfg.rms_eps, cfg.rope_theta
-    plen, max_pages = 13, 2
+    max_pages = (plen + 1 + PAGE - 1) // PAGE
     P = B * max_pages
     rng = np.random.default_rng(777 + B)
-    model = kvhp.LlamaModel(cfg, seed=31, max_ctx=64)
+    model = kvhp.LlamaModel(cfg, seed=31, max_ctx=max(64, plen + 1))
     pool = torch.zeros(L * 2 * Hkv * P * PAGE * D, dtype=torch.float16, device="cuda")
     bt = torch.from_numpy(rng.permutation(P).astype(np.int32).reshape(B, max_pages)).cuda()
     toks = torch.tensor([model.prefill_paged(rng.integers(0, V, plen).astype(np.int32), pool, P,
@@ -465,6 +472,8 @@ def test_batched_step_is_the_exported_operators(B):
     part = torch.empty(max(kvhp.gemv_rows_workspace_bytes(H, F, B), 16), dtype=torch.uint8,
                        device="cuda")
     assert (kvhp.gemv_rows_workspace_bytes(H, F, B) > 0) == (B == 17)
+    if shape == "d128":   # 33 splits of 128 keys: the per-query-head merge (>= 64 KB of partials)
+        assert kvhp.decode_workspace_bytes(B, Hq, Hkv, D, max_len) == 4 * B * Hq * 33 * (D + 2)
     for li in range(L):
         w = lambda which: model.tensor(li, which)
         kvhp.rmsnorm_qkv_rope_append_rows_tiled(
