@@ -1112,8 +1112,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(dbytes),
-                     "kernel": "decode_splitk_kernel<128,4,true,1> (append fused) + "
-                               "decode_merge_kernel<128,4>: one kvhp_paged_append_decode call",
+                     "kernel": "decode_splitk_kernel<128,4,true,1,false> (append fused) + "
+                               "decode_merge_kernel<128,4,false>: one kvhp_paged_append_decode call",
                      "avg_launch_us": round(r["step_us_region"], 2),
                      "per_step_event_us": {"median": round(r["step_us_median"], 2),
                                            "min": round(r["step_us_min"], 2),
