@@ -411,9 +411,10 @@ def test_decode_paged_graph_capture_needs_reserve():
     model.close()
 
 
-@pytest.mark.parametrize("shape,B,plen", [("d64", 3, 13), ("d64", 17, 13), ("d128", 2, 4190),
-                                          ("d32", 5, 20)])
-def test_batched_step_is_the_exported_operators(shape, B, plen):
+@pytest.mark.parametrize("shape,B,plen,ragged", [("d64", 3, 13, False), ("d64", 17, 13, False),
+                                                 ("d128", 2, 4190, False), ("d32", 5, 20, False),
+                                                 ("d64", 26, 700, True), ("d64", 9, 300, True)])
+def test_batched_step_is_the_exported_operators(shape, B, plen, ragged):
     """The runner's batched step keeps its hidden state, attention output
     and SwiGLU output row-tiled between launches; the exported operators
     take row-major activations.  One step of B sequences through
@@ -427,7 +428,10 @@ def test_batched_step_is_the_exported_operators(shape, B, plen):
     kernel (fixed chunks, four waves per split), B = 17 balanced splits
     and the per-KV-head merge, with the down projection split over K and
     15 padding rows; d128 B = 2 at 4191 keys 33 fixed splits and the
-    per-query-head merge; d32 the generic kernel."""
+    per-query-head merge; d32 the generic kernel.  Ragged: prompt lengths
+    drawn from 1..plen (balanced splits of different counts per sequence,
+    one-split and many-split sequences in one launch) and one idle row
+    (position -1, no keys: zero attention output, no page write)."""
     cfg = {"d64": _cfg(5632),
            "d128": kvhp.LlamaConfig(2048, 1024, 2, 8, 2, 128, 1024, 1e-5, 10000.0, 0),
            "d32": kvhp.LlamaConfig(2048, 256, 2, 8, 2, 32, 512, 1e-5, 10000.0, 0)}[shape]
@@ -440,11 +444,15 @@ def test_batched_step_is_the_exported_operators(shape, B, plen):
     model = kvhp.LlamaModel(cfg, seed=31, max_ctx=max(64, plen + 1))
     pool = torch.zeros(L * 2 * Hkv * P * PAGE * D, dtype=torch.float16, device="cuda")
     bt = torch.from_numpy(rng.permutation(P).astype(np.int32).reshape(B, max_pages)).cuda()
-    toks = torch.tensor([model.prefill_paged(rng.integers(0, V, plen).astype(np.int32), pool, P,
-                                             bt[b], max_pages)[0] for b in range(B)],
-                        dtype=torch.int32, device="cuda")
-    pos = torch.full((B,), plen, dtype=torch.int32, device="cuda")
-    sl = pos + 1
+    lens = rng.integers(1, plen + 1, B) if ragged else np.full(B, plen)
+    idle = B - 1 if ragged else -1
+    toks = torch.tensor([model.prefill_paged(rng.integers(0, V, int(lens[b])).astype(np.int32),
+                                             pool, P, bt[b], max_pages)[0] if b != idle else 0
+                         for b in range(B)], dtype=torch.int32, device="cuda")
+    pos = torch.tensor([int(lens[b]) if b != idle else -1 for b in range(B)], dtype=torch.int32,
+                       device="cuda")
+    sl = torch.tensor([int(lens[b]) + 1 if b != idle else 0 for b in range(B)], dtype=torch.int32,
+                      device="cuda")
     max_len = plen + 1
 
     pool_r = pool.clone()
@@ -471,7 +479,7 @@ def test_batched_step_is_the_exported_operators(shape, B, plen):
                      dtype=torch.uint8, device="cuda")
     part = torch.empty(max(kvhp.gemv_rows_workspace_bytes(H, F, B), 16), dtype=torch.uint8,
                        device="cuda")
-    assert (kvhp.gemv_rows_workspace_bytes(H, F, B) > 0) == (B == 17)
+    assert (kvhp.gemv_rows_workspace_bytes(H, F, B) > 0) == (B * F > 81920)
     if shape == "d128":   # 33 splits of 128 keys: the per-query-head merge (>= 64 KB of partials)
         assert kvhp.decode_workspace_bytes(B, Hq, Hkv, D, max_len) == 4 * B * Hq * 33 * (D + 2)
     for li in range(L):
