@@ -918,13 +918,15 @@ Plan make_plan(int batch, int num_kv_heads, int max_seq_len, int num_splits) {
     int s = num_splits;
     if (s <= 0) {
         // Measured on MI355X (B=1..32, L=512..64K, D=64/128): chunks of about
-        // L/64 tokens but never below 128, and at most ~6144 workgroups in
+        // L/64 tokens but never below 64, and at most ~6144 workgroups in
         // the grid.  Longer chunks starve the long sequences of a ragged
         // batch; shorter ones make the merge and per-workgroup set-up cost
-        // more than they hide.
+        // more than they hide.  (A floor of 128 instead: the config-5 step
+        // at ctx 2K 1522 vs 1549 tok/s, config 2 at 4K 12.6 vs 12.4 us; the
+        // balanced batches keep their own 128-key minimum.)
         const int64_t units = (int64_t)batch * num_kv_heads;
         int per_split = (max_seq_len + 63) / 64;
-        if (per_split < 128) per_split = 128;
+        if (per_split < 64) per_split = 64;
         per_split = (per_split + 63) / 64 * 64;
         s = (max_seq_len + per_split - 1) / per_split;
         const int64_t grid_cap = units >= 6144 ? 1 : 6144 / units;

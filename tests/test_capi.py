@@ -33,20 +33,20 @@ def test_kv_view_struct_layout_matches_header():
 
 
 def test_auto_split_policy():
-    # chunks of ~L/64 tokens but >= 128 (64-token multiples), grid of at most
+    # chunks of ~L/64 tokens but >= 64 (64-token multiples), grid of at most
     # 6144 workgroups, never more than 256 splits; batches below 8 with at
     # most 512 keys: one split (no merge launch)
     assert kvhp.decode_auto_splits(1, 8, 128, 64) == 1
-    expect = {(1, 8, 4096): 32, (1, 8, 16384): 64, (1, 8, 65536): 64, (1, 4, 2176): 17,
-              (1, 8, 512): 1, (7, 8, 512): 1, (8, 8, 512): 4, (1, 8, 513): 5, (32, 8, 8193): 22}
+    expect = {(1, 8, 4096): 64, (1, 8, 16384): 64, (1, 8, 65536): 64, (1, 4, 2176): 34,
+              (1, 8, 512): 1, (7, 8, 512): 1, (8, 8, 512): 8, (1, 8, 513): 9, (32, 8, 8193): 22}
     for (b, hkv, L), want in expect.items():
         assert kvhp.decode_auto_splits(b, hkv, 128, L) == want, (b, hkv, L)
     for b, hkv, L in [(1, 8, 100), (3, 2, 600), (64, 8, 32768), (1, 1, 1 << 20), (256, 32, 4096)]:
         s = kvhp.decode_auto_splits(b, hkv, 128, L)
         assert 1 <= s <= 256
         assert s == 1 or b * hkv * s <= 6144
-        chunk = -(-L // s)
-        assert s == 1 or chunk >= 64
+        chunk = -(-L // s) + 63 & ~63    # tokens per split, 64-token multiples
+        assert s == -(-L // chunk) and (s == 1 or chunk >= 64)
 
 
 def test_workspace_sizing():
