@@ -1264,7 +1264,10 @@ int decode_attention_impl(const void* q, const kvhp_kv_view* kv, const kvhp_kv_v
     // explicit split count keeps the fixed chunk: exactly that split.
     a.batch = batch;
     a.balance = num_splits <= 0 && batch >= 8 ? 1 : 0;   // unit count set per kernel at launch
-    a.min_chunk = 128;
+    // Fewest keys per split: 64 from 16 sequences, 128 below (the config-5
+    // batched runner at ctx 2K with 64: B = 32 1.365 vs 1.384 ms per step,
+    // B = 8 0.986 vs 0.974 ms; config 3's splits are longer either way).
+    a.min_chunk = batch >= 16 ? 64 : 128;
     a.max_chunk = paged ? kMaxPagedChunk : (a.cap + kPage - 1) / kPage * kPage;
     if (a.max_chunk < plan.chunk) a.max_chunk = plan.chunk;
     const size_t need = workspace_bytes_for(batch, hq, hkv, d, plan);
