@@ -109,11 +109,12 @@ def test_prefill_batched():
         assert_attn_close(got[i], ref, f"batch {i}")
 
 
-# Short prompts with G <= 4 run one pass per pair of query blocks (the short
-# block's units first share key tiles with the long block, then help with the
-# long block's tiles).  Cases: G = 1 / 2 / 4, D = 64 / 128, odd block counts
-# (the middle pair is a single block), partial last tiles, a pair whose two
-# blocks end in the same tile, and a batch.
+# Short prompts with G <= 4 run the two-key-group kernel (two wave groups
+# split every 64-key tile and merge their softmax states at the end), with
+# causal blocks paired into one workgroup (two passes) once the pairs fill the
+# CUs, one block per workgroup below that.  Cases: G = 1 / 2 / 4, D = 64 /
+# 128, odd block counts (the middle pair is a single block), partial last
+# tiles, a pair whose two blocks end in the same tile, and a batch.
 @pytest.mark.parametrize("s,hq,hkv,d,batch", [
     (1, 4, 4, 128, 1), (96, 4, 4, 128, 1), (333, 4, 4, 64, 1), (1000, 4, 4, 128, 1),
     (100, 8, 4, 128, 1), (513, 8, 4, 64, 1), (640, 8, 4, 128, 1),
