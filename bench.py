@@ -807,42 +807,39 @@ def run_config4(torch, kvhp, sizes=(512, 2048, 4096, 8192), reps=10, attention_o
     fl = Flusher(torch)
     stream = torch.cuda.current_stream()
 
-    def settle(fn, seconds=0.1):
-        # The chip's clocks ramp up over tens of ms of sustained work: from
-        # idle an S=2048 call takes 55-57 us and settles at ~46.5 us after
-        # ~40 ms of back-to-back calls.  Calls for `seconds` first, so that
-        # the timed runs see the sustained-load clock; returns the median
-        # time of the first 5 calls (the cold start) in us.
-        torch.cuda.synchronize()
-        first = []
-        for _ in range(5):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            fn()
-            e1.record(stream)
-            e1.synchronize()
-            first.append(e0.elapsed_time(e1) * 1e3)
-        t0 = time.perf_counter()
-        while time.perf_counter() - t0 < seconds:
-            for _ in range(10):
-                fn()
-            torch.cuda.synchronize()
-        return float(np.median(first))
-
-    def back_to_back(fn):
+    def back_to_back(fn, seconds=0.1):
         # MFMA-bound: timed back to back (the inputs come straight from the
-        # projection GEMMs in a serving step, cache-warm), 5 runs of `reps`
-        # calls under one event pair, after the settle phase
-        warm = []
+        # projection GEMMs in a serving step, cache-warm).  The chip's clocks
+        # ramp up over tens of ms of sustained work (from idle an S=2048 call
+        # takes 52-57 us and ~46.5-48 us after ~40 ms), and an idle gap drops
+        # them again: so ~`seconds` of the same calls are enqueued first and
+        # the 5 timed runs of `reps` calls (one event pair each) right behind
+        # them, with no host synchronisation in between.  Returns the
+        # (median, mean, min, max) per-call time of the runs and the mean of
+        # 5 calls under one event pair made first (the cold start), in us.
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        fn()   # first launch of the section (lazy set-up outside the cold figure)
+        torch.cuda.synchronize()
+        e0.record(stream)
         for _ in range(5):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        cold = e0.elapsed_time(e1) * 1e3 / 5
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(5)]
+        for _ in range(max(1, int(seconds * 1e6 / max(cold, 1.0)))):
+            fn()
+        for e0, e1 in evs:
             e0.record(stream)
             for _ in range(reps):
                 fn()
             e1.record(stream)
-            e1.synchronize()
-            warm.append(e0.elapsed_time(e1) * 1e3 / reps)
-        return (float(np.median(warm)), float(np.mean(warm)), float(np.min(warm)), float(np.max(warm)))
+        torch.cuda.synchronize()
+        warm = [e0.elapsed_time(e1) * 1e3 / reps for e0, e1 in evs]
+        return (float(np.median(warm)), float(np.mean(warm)), float(np.min(warm)),
+                float(np.max(warm))), cold
 
     for s in sizes:
         g = torch.Generator(device="cuda").manual_seed(s)
@@ -864,16 +861,14 @@ def run_config4(torch, kvhp, sizes=(512, 2048, 4096, 8192), reps=10, attention_o
 
         flops = 2.0 * d * hq * s * (s + 1)
         pct = lambda us: round(flops / us / 1e6 / FP16_PEAK_TFLOPS * 100, 2)
-        cold = settle(paged)
-        t = back_to_back(paged)
+        t, cold = back_to_back(paged)
         tfl = time_op(torch, paged, reps, fl)
         row = {"S": s, **spread(t), "TFLOP/s": round(flops / t[0] / 1e6, 1),
                "pct_fp16_peak": pct(t[0]),
                "flushed": {**spread(tfl), "pct_fp16_peak": pct(tfl[0])},
                "cold_start": {"us": round(cold, 2), "pct_fp16_peak": pct(cold)}}
         if attention_only:
-            settle(plain)
-            ta = back_to_back(plain)
+            ta, _ = back_to_back(plain)
             tafl = time_op(torch, plain, reps, fl)
             row["attention_only"] = {**spread(ta), "pct_fp16_peak": pct(ta[0]),
                                      "flushed": {**spread(tafl), "pct_fp16_peak": pct(tafl[0])}}
@@ -881,9 +876,10 @@ def run_config4(torch, kvhp, sizes=(512, 2048, 4096, 8192), reps=10, attention_o
     return {"workload": "config4: causal prefill B=1, 32/8 heads, D=128, fp16 in / fp32 acc, "
                         "K/V written into 16-token pages (seeded random page order) as the "
                         "prefill runs (kvhp_flash_prefill_paged); back-to-back calls (median "
-                        "of 5 runs) after 0.1 s of the same calls (the clocks settle under "
-                        "sustained load), flushed single calls beside; cold_start = the "
-                        "median of the first 5 calls after the section's set-up; "
+                        "of 5 runs) enqueued right behind ~0.1 s of the same calls (the "
+                        "clocks settle under sustained load), flushed single calls beside; "
+                        "cold_start = 5 calls back to back right after the section's set-up "
+                        "(mean); "
                         "attention_only = the same prefill without the page writes",
             "rows": rows}
 
